@@ -1,0 +1,171 @@
+/*
+ * nve_kernels.h -- C ABI of libnve_hip.so, the MI355X (gfx950) quantized decode GEMV
+ * library.  Drop-in for the launchers that genovationtech/nve binds in
+ * src/cuda_kernels.rs (extern block, lines 57-289) and defines in cuda/nve_kernels.cu.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer the caller allocated; nothing here allocates
+ *     device memory, and every launch is asynchronous on `stream` (a hipStream_t;
+ *     NULL = the default stream).
+ *   - Weights use the reference's GPU layout (QuantizedTensor::extract_for_gpu,
+ *     src/quantize.rs:437-463): nibbles u8 [N, K/2], byte j of each 32-weight block
+ *     = element j (low nibble) | element j+16 (high nibble); scales f32 [N, K/32];
+ *     weight value = (nibble - 8) * scale.
+ *   - The `nve_hip_*` functions return an nve_status (0 = success, > 0 = a
+ *     hipError_t from the launch, < 0 = an argument error below).  The drop-in
+ *     `void` launchers with the reference's names call them, and on failure print
+ *     one line to stderr and record the status for nve_hip_last_status().
+ *   - Alignment: nibbles and int8 activations 16-byte aligned; scales 4-byte aligned;
+ *     fp16/bf16 vectors 16-byte aligned.
+ *   - Limits: K % 32 == 0, 32 <= K <= NVE_MAX_K, 1 <= N; M <= NVE_MAX_M.
+ */
+#ifndef NVE_KERNELS_H
+#define NVE_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+#define NVE_OK 0
+#define NVE_ERR_NULL (-1)      /* a required pointer is NULL */
+#define NVE_ERR_SHAPE (-2)     /* N < 1, K % 32 != 0, K out of range, M out of range */
+#define NVE_ERR_ALIGN (-3)     /* a pointer violates the alignment above */
+#define NVE_ERR_DTYPE (-4)     /* unsupported dtype / mode code */
+#define NVE_ERR_TOO_LARGE (-5) /* a size exceeds a documented maximum */
+
+/* ---- dtype codes ------------------------------------------------------------ */
+#define NVE_DT_F16 0
+#define NVE_DT_BF16 1
+#define NVE_DT_F32 2
+
+/* ---- activation-scale modes for the W4A8 kernels ------------------------- */
+#define NVE_XS_GROUP32_F32 0 /* one f32 scale per 32 activations (reference mode) */
+#define NVE_XS_ROW_BF16 1    /* one bf16 scale per activation row (per-token mode) */
+
+#define NVE_MAX_K 32768
+#define NVE_MAX_M 16
+
+/* =========================================================================
+ * Drop-in launchers: same symbol names and argument order as the reference.
+ * ========================================================================= */
+
+/* Replaces nve_quantize_f16_q8 (cuda/nve_kernels.cu:747-757; Rust decl
+ * src/cuda_kernels.rs:251-257).  x fp16 [K] -> xq int8 [K], scales f32 [K/32]:
+ * per group amax; scale = amax > 0 ? amax/127 : 1; q = clamp(rne(x/scale*), +-127)
+ * with IEEE division (the reference's --use_fast_math reciprocal is not copied). */
+void nve_quantize_f16_q8(const uint16_t *x, int8_t *xq, float *scales, int K, void *stream);
+
+/* Replaces nve_matvec_w4a8 (cuda/nve_kernels.cu:880-894; Rust decl
+ * src/cuda_kernels.rs:261-270).  out fp16 [N] = sum_b ws[n,b] * xs[b] * acc[n,b],
+ * acc = exact int32 sum over the block of (nibble - 8) * xq. */
+void nve_matvec_w4a8(const int8_t *xq, const float *xq_scales, const uint8_t *nibbles,
+                     const float *wt_scales, uint16_t *out, int N, int K, void *stream);
+
+/* Replaces nve_matvec_w4a16 (cuda/nve_kernels.cu:373-388; Rust decl
+ * src/cuda_kernels.rs:117-130).  out fp16 [N] = sum_k x[k] * awq[k] * (nib-8) * s;
+ * awq may be NULL. */
+void nve_matvec_w4a16(const uint16_t *x, const uint8_t *nibbles, const float *scales,
+                      const float *awq, uint16_t *out, int N, int K, void *stream);
+
+/* Replaces nve_qkv_matvec_w4a16 (cuda/nve_kernels.cu:680-700; Rust decl
+ * src/cuda_kernels.rs:170-180): the three W4A16 projections sharing x in one launch. */
+void nve_qkv_matvec_w4a16(const uint16_t *x, const uint8_t *q_nib, const float *q_sc,
+                          const float *q_awq, int Nq, const uint8_t *k_nib, const float *k_sc,
+                          const float *k_awq, int Nk, const uint8_t *v_nib, const float *v_sc,
+                          const float *v_awq, int Nv, uint16_t *q_out, uint16_t *k_out,
+                          uint16_t *v_out, int K, void *stream);
+
+/* =========================================================================
+ * Status-returning entry points (dtype-generic twins of the launchers above).
+ * ========================================================================= */
+
+/* Twin of nve_quantize_f16_q8 for x of dtype x_dtype (F16, BF16 or F32), group-32
+ * f32 scales.  M rows of K activations each (xq [M,K], scales [M,K/32]). */
+int nve_hip_quantize_q8(const void *x, int x_dtype, int M, int K, int8_t *xq, float *scales,
+                        void *stream);
+
+/* Per-token variant (no reference counterpart; the batched configurations ask for
+ * it): one bf16 scale per row.  s = amax > 0 ? amax/127 : 1; sb = bf16_rne(s);
+ * q = clamp(rne(x * (1/float(sb))), +-127).  xq [M,K], scales_bf16 [M]. */
+int nve_hip_quantize_q8_rows(const void *x, int x_dtype, int M, int K, int8_t *xq,
+                             uint16_t *scales_bf16, void *stream);
+
+/* Twin of nve_matvec_w4a8 with a selectable output dtype (F16, BF16 or F32; the
+ * F32 output is the value before any rounding to 16 bits). */
+int nve_hip_matvec_w4a8(const int8_t *xq, const float *xq_scales, const uint8_t *nibbles,
+                        const float *wt_scales, void *out, int out_dtype, int N, int K,
+                        void *stream);
+
+/* Fused Q/K/V W4A8: the three projections that share one quantized activation
+ * vector in one launch (the reference issues three nve_matvec_w4a8 launches,
+ * src/gpu_layer.rs:659-661). */
+int nve_hip_qkv_matvec_w4a8(const int8_t *xq, const float *xq_scales, const uint8_t *q_nib,
+                            const float *q_sc, int Nq, const uint8_t *k_nib, const float *k_sc,
+                            int Nk, const uint8_t *v_nib, const float *v_sc, int Nv, void *q_out,
+                            void *k_out, void *v_out, int out_dtype, int K, void *stream);
+
+/* Batched W4A8 (small-batch decode, 1 <= M <= NVE_MAX_M).  xq [M,K]; xs_mode
+ * NVE_XS_GROUP32_F32: xq_scales f32 [M, K/32]; NVE_XS_ROW_BF16: bf16 [M].
+ * out [M, N] of out_dtype.  M >= 4 runs on int8 MFMA; smaller M on v_dot4. */
+int nve_hip_matvec_w4a8_batched(int M, const int8_t *xq, const void *xq_scales, int xs_mode,
+                                const uint8_t *nibbles, const float *wt_scales, void *out,
+                                int out_dtype, int N, int K, void *stream);
+
+/* Debug export of the exact int32 block accumulators of the W4A8 kernels:
+ * acc [N, K/32], acc[n,b] = sum over block b of (nibble - 8) * xq.  Computed by the
+ * same device routine the GEMV kernels use (cuda/nve_kernels.cu:835-853). */
+int nve_hip_w4a8_block_acc(const int8_t *xq, const uint8_t *nibbles, int32_t *acc, int N,
+                           int K, void *stream);
+
+/* Twin of nve_matvec_w4a16: x_dtype F16 or BF16, awq nullable, out_dtype F16, BF16
+ * or F32. */
+int nve_hip_matvec_w4a16(const void *x, int x_dtype, const uint8_t *nibbles,
+                         const float *scales, const float *awq, void *out, int out_dtype,
+                         int N, int K, void *stream);
+
+/* Twin of nve_qkv_matvec_w4a16 with dtype codes. */
+int nve_hip_qkv_matvec_w4a16(const void *x, int x_dtype, const uint8_t *q_nib,
+                             const float *q_sc, const float *q_awq, int Nq,
+                             const uint8_t *k_nib, const float *k_sc, const float *k_awq,
+                             int Nk, const uint8_t *v_nib, const float *v_sc,
+                             const float *v_awq, int Nv, void *q_out, void *k_out,
+                             void *v_out, int out_dtype, int K, void *stream);
+
+/* ---- weight preparation (run once per layer upload) ------------------------ */
+
+/* QuantizedTensor::from_f32 / from_compact + extract_for_gpu on the device
+ * (src/quantize.rs:347-375, 242-268, 711-731, 437-463): w [N,K] of w_dtype (F32,
+ * BF16 or F16) -> nibbles in GPU order + f32 scales, bit-identical to the reference
+ * quantizer (f32::round half away from zero, saturating `as i8`). */
+int nve_hip_q4_quantize(const void *w, int w_dtype, int N, int K, uint8_t *nibbles,
+                        float *scales, void *stream);
+
+/* QuantizedTensor::extract_for_gpu (src/quantize.rs:437-463) on the device: the
+ * reference's CPU Q4_0 bytes (20-byte blocks [f32 scale][16 B, byte i = e_2i |
+ * e_2i+1 << 4], row-major) -> nibbles in GPU order + scales.  q4_blocks 4-byte
+ * aligned. */
+int nve_hip_q4_repack(const uint8_t *q4_blocks, int N, int K, uint8_t *nibbles,
+                      float *scales, void *stream);
+
+/* ---- per-layer precision dispatch (src/gpu_layer.rs:1013-1025) -------------- */
+/* Returns 1 (W4A8) when NVE_NO_W4A8 is unset and layer_importance < threshold,
+ * where threshold = NVE_W4A8_THRESHOLD parsed as a double, default 0.7; else 0. */
+int nve_use_w4a8(double layer_importance);
+
+/* ---- measurement and diagnostics ------------------------------------------ */
+/* Read-only HBM streaming probe: reads `bytes` (multiple of 16, 16-byte aligned)
+ * from buf and writes one f32 per workgroup-slot into sink[0..1023]. */
+int nve_hip_stream_read(const void *buf, size_t bytes, float *sink, void *stream);
+int nve_hip_last_status(void);
+const char *nve_hip_status_string(int status);
+/* Library version string. */
+const char *nve_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

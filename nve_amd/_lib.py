@@ -1,0 +1,80 @@
+"""ctypes binding of libnve_hip.so (the C ABI in include/nve_kernels.h).
+
+Loading fails loudly when the library has not been built: the product path has no
+CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libnve_hip.so"
+
+# status / dtype / mode codes (include/nve_kernels.h)
+NVE_OK = 0
+NVE_ERR_NULL = -1
+NVE_ERR_SHAPE = -2
+NVE_ERR_ALIGN = -3
+NVE_ERR_DTYPE = -4
+NVE_ERR_TOO_LARGE = -5
+DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+XS_GROUP32_F32, XS_ROW_BF16 = 0, 1
+MAX_K = 32768
+MAX_M = 16
+
+_p = C.c_void_p
+_i = C.c_int
+
+# name -> (restype, argtypes), every symbol include/nve_kernels.h declares
+SIGNATURES: dict[str, tuple] = {
+    "nve_quantize_f16_q8": (None, [_p, _p, _p, _i, _p]),
+    "nve_matvec_w4a8": (None, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "nve_matvec_w4a16": (None, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "nve_qkv_matvec_w4a16": (None, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _p]),
+    "nve_hip_quantize_q8": (_i, [_p, _i, _i, _i, _p, _p, _p]),
+    "nve_hip_quantize_q8_rows": (_i, [_p, _i, _i, _i, _p, _p, _p]),
+    "nve_hip_matvec_w4a8": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "nve_hip_qkv_matvec_w4a8": (_i, [_p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
+    "nve_hip_matvec_w4a8_batched": (_i, [_i, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
+    "nve_hip_w4a8_block_acc": (_i, [_p, _p, _p, _i, _i, _p]),
+    "nve_hip_matvec_w4a16": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "nve_hip_qkv_matvec_w4a16": (_i, [_p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
+    "nve_hip_q4_quantize": (_i, [_p, _i, _i, _i, _p, _p, _p]),
+    "nve_hip_q4_repack": (_i, [_p, _i, _i, _p, _p, _p]),
+    "nve_use_w4a8": (_i, [C.c_double]),
+    "nve_hip_stream_read": (_i, [_p, C.c_size_t, _p, _p]),
+    "nve_hip_last_status": (_i, []),
+    "nve_hip_status_string": (C.c_char_p, [_i]),
+    "nve_hip_version": (C.c_char_p, []),
+}
+
+_lib: C.CDLL | None = None
+
+
+class NveError(RuntimeError):
+    def __init__(self, fn: str, status: int):
+        msg = lib().nve_hip_status_string(status).decode()
+        super().__init__(f"{fn}: {msg} (status {status})")
+        self.status = status
+
+
+def lib() -> C.CDLL:
+    """Load libnve_hip.so (raises if it is missing: there is no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != NVE_OK:
+        raise NveError(fn, status)

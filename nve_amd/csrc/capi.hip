@@ -1,0 +1,296 @@
+// capi.hip -- the extern "C" boundary of libnve_hip.so (declared in
+// include/nve_kernels.h): argument validation, status codes, and the drop-in
+// launchers with the reference's names (cuda/nve_kernels.cu:373, 680, 747, 880).
+#include <errno.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "common.h"
+#include "w4_launch.h"
+
+namespace nve_host {
+
+static thread_local int g_last_status = NVE_OK;
+
+int set_status(int st) {
+  g_last_status = st;
+  return st;
+}
+
+int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NVE_OK : (int)e;
+}
+
+static int from_hip(hipError_t e) { return set_status(e == hipSuccess ? NVE_OK : (int)e); }
+
+static bool dtype_ok(int dt) { return dt == NVE_DT_F16 || dt == NVE_DT_BF16 || dt == NVE_DT_F32; }
+
+// Common GEMV argument checks.
+static int check_gemv(const void* nib, const void* sc, const void* out, int N, int K) {
+  if (!nib || !sc || !out) return NVE_ERR_NULL;
+  if (N < 1 || K < 32 || K % 32 != 0) return NVE_ERR_SHAPE;
+  if (K > NVE_MAX_K) return NVE_ERR_TOO_LARGE;
+  if (!aligned(nib, 16) || !aligned(sc, 4) || !aligned(out, 2)) return NVE_ERR_ALIGN;
+  return NVE_OK;
+}
+
+static void report(const char* fn, int st) {
+  if (st != NVE_OK) fprintf(stderr, "nve_hip: %s failed: %s (%d)\n", fn, nve_hip_status_string(st), st);
+}
+
+hipError_t launch_q8_group(const void* x, int xdt, size_t total, int8_t* xq, float* scales,
+                           hipStream_t stream);
+hipError_t launch_q8_rows(const void* x, int xdt, int M, int K, int8_t* xq, uint16_t* scales,
+                          hipStream_t stream);
+hipError_t launch_q4_quantize(const void* w, int wdt, size_t nblocks, uint8_t* nib, float* scales,
+                              hipStream_t stream);
+hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, float* scales,
+                            hipStream_t stream);
+hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream);
+hipError_t launch_w4a8_batched(int M, const int8_t* xq, const void* xs, int xs_mode,
+                               const uint8_t* nib, const float* ws, void* out, int out_dt, int N,
+                               int K, hipStream_t stream);
+
+}  // namespace nve_host
+
+using namespace nve_host;
+
+extern "C" {
+
+const char* nve_hip_status_string(int st) {
+  switch (st) {
+    case NVE_OK: return "ok";
+    case NVE_ERR_NULL: return "null pointer argument";
+    case NVE_ERR_SHAPE: return "invalid shape (need N >= 1, K % 32 == 0, 32 <= K, 1 <= M <= NVE_MAX_M)";
+    case NVE_ERR_ALIGN: return "misaligned pointer";
+    case NVE_ERR_DTYPE: return "unsupported dtype or mode";
+    case NVE_ERR_TOO_LARGE: return "size exceeds a documented maximum";
+    default: return st > 0 ? hipGetErrorString((hipError_t)st) : "unknown error";
+  }
+}
+
+int nve_hip_last_status(void) { return g_last_status; }
+
+const char* nve_hip_version(void) { return "nve_hip 0.1.0 gfx950"; }
+
+// ---- activation quantization --------------------------------------------------
+int nve_hip_quantize_q8(const void* x, int x_dtype, int M, int K, int8_t* xq, float* scales,
+                        void* stream) {
+  if (!x || !xq || !scales) return set_status(NVE_ERR_NULL);
+  if (!dtype_ok(x_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (M < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(x, 16) || !aligned(xq, 4) || !aligned(scales, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_q8_group(x, x_dtype, (size_t)M * K, xq, scales, (hipStream_t)stream));
+}
+
+int nve_hip_quantize_q8_rows(const void* x, int x_dtype, int M, int K, int8_t* xq,
+                             uint16_t* scales_bf16, void* stream) {
+  if (!x || !xq || !scales_bf16) return set_status(NVE_ERR_NULL);
+  if (!dtype_ok(x_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (M < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(x, 16) || !aligned(xq, 4) || !aligned(scales_bf16, 2)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_q8_rows(x, x_dtype, M, K, xq, scales_bf16, (hipStream_t)stream));
+}
+
+// ---- W4A8 --------------------------------------------------------------------------
+int nve_hip_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t* nibbles,
+                        const float* wt_scales, void* out, int out_dtype, int N, int K,
+                        void* stream) {
+  if (!xq || !xq_scales) return set_status(NVE_ERR_NULL);
+  int st = check_gemv(nibbles, wt_scales, out, N, K);
+  if (st != NVE_OK) return set_status(st);
+  if (!dtype_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (!aligned(xq, 16) || !aligned(xq_scales, 4) || (out_dtype == NVE_DT_F32 && !aligned(out, 4)))
+    return set_status(NVE_ERR_ALIGN);
+  W4Segs s{};
+  s.nseg = 1;
+  s.nib[0] = nibbles;
+  s.sc[0] = wt_scales;
+  s.out[0] = out;
+  s.n[0] = N;
+  return from_hip(launch_w4a8(xq, xq_scales, s, out_dtype, K, (hipStream_t)stream));
+}
+
+int nve_hip_qkv_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t* q_nib,
+                            const float* q_sc, int Nq, const uint8_t* k_nib, const float* k_sc,
+                            int Nk, const uint8_t* v_nib, const float* v_sc, int Nv, void* q_out,
+                            void* k_out, void* v_out, int out_dtype, int K, void* stream) {
+  if (!xq || !xq_scales) return set_status(NVE_ERR_NULL);
+  const uint8_t* nibs[3] = {q_nib, k_nib, v_nib};
+  const float* scs[3] = {q_sc, k_sc, v_sc};
+  void* outs[3] = {q_out, k_out, v_out};
+  const int ns[3] = {Nq, Nk, Nv};
+  W4Segs s{};
+  s.nseg = 3;
+  for (int i = 0; i < 3; ++i) {
+    int st = check_gemv(nibs[i], scs[i], outs[i], ns[i], K);
+    if (st != NVE_OK) return set_status(st);
+    if (out_dtype == NVE_DT_F32 && !aligned(outs[i], 4)) return set_status(NVE_ERR_ALIGN);
+    s.nib[i] = nibs[i];
+    s.sc[i] = scs[i];
+    s.out[i] = outs[i];
+    s.n[i] = ns[i];
+  }
+  if (!dtype_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (!aligned(xq, 16) || !aligned(xq_scales, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a8(xq, xq_scales, s, out_dtype, K, (hipStream_t)stream));
+}
+
+int nve_hip_w4a8_block_acc(const int8_t* xq, const uint8_t* nibbles, int32_t* acc, int N, int K,
+                           void* stream) {
+  if (!xq || !nibbles || !acc) return set_status(NVE_ERR_NULL);
+  if (N < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(xq, 16) || !aligned(nibbles, 16) || !aligned(acc, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a8_block_acc(xq, nibbles, acc, N, K, (hipStream_t)stream));
+}
+
+int nve_hip_matvec_w4a8_batched(int M, const int8_t* xq, const void* xq_scales, int xs_mode,
+                                const uint8_t* nibbles, const float* wt_scales, void* out,
+                                int out_dtype, int N, int K, void* stream) {
+  if (!xq || !xq_scales) return set_status(NVE_ERR_NULL);
+  int st = check_gemv(nibbles, wt_scales, out, N, K);
+  if (st != NVE_OK) return set_status(st);
+  if (M < 1 || M > NVE_MAX_M) return set_status(NVE_ERR_SHAPE);
+  if (!dtype_ok(out_dtype) || (xs_mode != NVE_XS_GROUP32_F32 && xs_mode != NVE_XS_ROW_BF16))
+    return set_status(NVE_ERR_DTYPE);
+  if (!aligned(xq, 16) || !aligned(xq_scales, xs_mode == NVE_XS_ROW_BF16 ? 2 : 4) ||
+      (out_dtype == NVE_DT_F32 && !aligned(out, 4)))
+    return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a8_batched(M, xq, xq_scales, xs_mode, nibbles, wt_scales, out, out_dtype, N,
+                                      K, (hipStream_t)stream));
+}
+
+// ---- W4A16 --------------------------------------------------------------------------
+int nve_hip_matvec_w4a16(const void* x, int x_dtype, const uint8_t* nibbles, const float* scales,
+                         const float* awq, void* out, int out_dtype, int N, int K, void* stream) {
+  if (!x) return set_status(NVE_ERR_NULL);
+  int st = check_gemv(nibbles, scales, out, N, K);
+  if (st != NVE_OK) return set_status(st);
+  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !dtype_ok(out_dtype))
+    return set_status(NVE_ERR_DTYPE);
+  if (!aligned(x, 16) || (awq && !aligned(awq, 16)) || (out_dtype == NVE_DT_F32 && !aligned(out, 4)))
+    return set_status(NVE_ERR_ALIGN);
+  W4Segs s{};
+  s.nseg = 1;
+  s.nib[0] = nibbles;
+  s.sc[0] = scales;
+  s.awq[0] = awq;
+  s.out[0] = out;
+  s.n[0] = N;
+  return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
+}
+
+int nve_hip_qkv_matvec_w4a16(const void* x, int x_dtype, const uint8_t* q_nib, const float* q_sc,
+                             const float* q_awq, int Nq, const uint8_t* k_nib, const float* k_sc,
+                             const float* k_awq, int Nk, const uint8_t* v_nib, const float* v_sc,
+                             const float* v_awq, int Nv, void* q_out, void* k_out, void* v_out,
+                             int out_dtype, int K, void* stream) {
+  if (!x) return set_status(NVE_ERR_NULL);
+  const uint8_t* nibs[3] = {q_nib, k_nib, v_nib};
+  const float* scs[3] = {q_sc, k_sc, v_sc};
+  const float* awqs[3] = {q_awq, k_awq, v_awq};
+  void* outs[3] = {q_out, k_out, v_out};
+  const int ns[3] = {Nq, Nk, Nv};
+  W4Segs s{};
+  s.nseg = 3;
+  for (int i = 0; i < 3; ++i) {
+    int st = check_gemv(nibs[i], scs[i], outs[i], ns[i], K);
+    if (st != NVE_OK) return set_status(st);
+    if ((awqs[i] && !aligned(awqs[i], 16)) || (out_dtype == NVE_DT_F32 && !aligned(outs[i], 4)))
+      return set_status(NVE_ERR_ALIGN);
+    s.nib[i] = nibs[i];
+    s.sc[i] = scs[i];
+    s.awq[i] = awqs[i];
+    s.out[i] = outs[i];
+    s.n[i] = ns[i];
+  }
+  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !dtype_ok(out_dtype))
+    return set_status(NVE_ERR_DTYPE);
+  if (!aligned(x, 16)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
+}
+
+// ---- weight preparation -------------------------------------------------------------
+int nve_hip_q4_quantize(const void* w, int w_dtype, int N, int K, uint8_t* nibbles, float* scales,
+                        void* stream) {
+  if (!w || !nibbles || !scales) return set_status(NVE_ERR_NULL);
+  if (!dtype_ok(w_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (N < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(w, w_dtype == NVE_DT_F32 ? 4 : 2) || !aligned(nibbles, 16) || !aligned(scales, 4))
+    return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_q4_quantize(w, w_dtype, (size_t)N * (K / 32), nibbles, scales, (hipStream_t)stream));
+}
+
+int nve_hip_q4_repack(const uint8_t* q4_blocks, int N, int K, uint8_t* nibbles, float* scales,
+                      void* stream) {
+  if (!q4_blocks || !nibbles || !scales) return set_status(NVE_ERR_NULL);
+  if (N < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(q4_blocks, 4) || !aligned(nibbles, 16) || !aligned(scales, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_q4_repack(q4_blocks, (size_t)N * (K / 32), nibbles, scales, (hipStream_t)stream));
+}
+
+// ---- dispatch -------------------------------------------------------------------------
+// src/gpu_layer.rs:1013-1025: NVE_NO_W4A8 set (any value) -> W4A16; otherwise W4A8
+// when importance < NVE_W4A8_THRESHOLD, a double parsed like Rust's str::parse::<f64>
+// (no surrounding whitespace, no hex), falling back to 0.7 when unset or unparsable.
+static bool parse_f64_strict(const char* s, double* out) {
+  if (!s || !*s) return false;
+  const char* p = s;
+  if (*p == '+' || *p == '-') ++p;
+  if (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r' || *p == '\f' || *p == '\v') return false;
+  if (p[0] == '0' && (p[1] == 'x' || p[1] == 'X')) return false;
+  if (*s == ' ' || *s == '\t' || *s == '\n') return false;
+  char* end = nullptr;
+  errno = 0;
+  const double v = strtod(s, &end);
+  if (end == s || *end != '\0') return false;
+  *out = v;
+  return true;
+}
+
+int nve_use_w4a8(double layer_importance) {
+  if (getenv("NVE_NO_W4A8") != nullptr) return 0;
+  double threshold = 0.7;
+  double parsed;
+  if (parse_f64_strict(getenv("NVE_W4A8_THRESHOLD"), &parsed)) threshold = parsed;
+  return layer_importance < threshold ? 1 : 0;
+}
+
+// ---- measurement ----------------------------------------------------------------------
+int nve_hip_stream_read(const void* buf, size_t bytes, float* sink, void* stream) {
+  if (!buf || !sink) return set_status(NVE_ERR_NULL);
+  if (bytes == 0 || bytes % 16 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(buf, 16) || !aligned(sink, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_stream_read(buf, bytes, sink, (hipStream_t)stream));
+}
+
+// ---- drop-in launchers (reference names and argument order) ----------------------
+void nve_quantize_f16_q8(const uint16_t* x, int8_t* xq, float* scales, int K, void* stream) {
+  report("nve_quantize_f16_q8", nve_hip_quantize_q8(x, NVE_DT_F16, 1, K, xq, scales, stream));
+}
+
+void nve_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t* nibbles,
+                     const float* wt_scales, uint16_t* out, int N, int K, void* stream) {
+  report("nve_matvec_w4a8",
+         nve_hip_matvec_w4a8(xq, xq_scales, nibbles, wt_scales, out, NVE_DT_F16, N, K, stream));
+}
+
+void nve_matvec_w4a16(const uint16_t* x, const uint8_t* nibbles, const float* scales,
+                      const float* awq, uint16_t* out, int N, int K, void* stream) {
+  report("nve_matvec_w4a16",
+         nve_hip_matvec_w4a16(x, NVE_DT_F16, nibbles, scales, awq, out, NVE_DT_F16, N, K, stream));
+}
+
+void nve_qkv_matvec_w4a16(const uint16_t* x, const uint8_t* q_nib, const float* q_sc,
+                          const float* q_awq, int Nq, const uint8_t* k_nib, const float* k_sc,
+                          const float* k_awq, int Nk, const uint8_t* v_nib, const float* v_sc,
+                          const float* v_awq, int Nv, uint16_t* q_out, uint16_t* k_out,
+                          uint16_t* v_out, int K, void* stream) {
+  report("nve_qkv_matvec_w4a16",
+         nve_hip_qkv_matvec_w4a16(x, NVE_DT_F16, q_nib, q_sc, q_awq, Nq, k_nib, k_sc, k_awq, Nk, v_nib,
+                                  v_sc, v_awq, Nv, q_out, k_out, v_out, NVE_DT_F16, K, stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// common.h -- shared device helpers for the gfx950 W4A8 / W4A16 decode GEMV library.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, DPP cross-lane
+// moves, v_dot4_i32_i8 / v_dot2_f32_f16 dot instructions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nve_kernels.h"
+
+namespace nve {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 32;  // Q4_0 / Q8 group size (weights and activations)
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+
+// ---- wavefront reductions (DPP; the total lands in lane 63) ----------------
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror, then
+// row_bcast:15 into rows 1/3 and row_bcast:31 into rows 2/3.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Sum over all 64 lanes; result valid in lane 63.
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v += dpp_mov<0xB1>(v);        // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);        // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);       // row_half_mirror
+  v += dpp_mov<0x140>(v);       // row_mirror
+  v += dpp_mov<0x142, 0xA>(v);  // row_bcast:15 -> rows 1,3
+  v += dpp_mov<0x143, 0xC>(v);  // row_bcast:31 -> rows 2,3
+  return v;
+}
+
+// Sum over all 64 lanes, broadcast to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(v)), 63));
+}
+
+// Reductions within aligned groups of 4 lanes (all 4 lanes get the result).
+__device__ __forceinline__ int quad_sum_i(int v) {
+  v += dpp_mov_i<0xB1>(v);
+  v += dpp_mov_i<0x4E>(v);
+  return v;
+}
+__device__ __forceinline__ float quad_max_f(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  return v;
+}
+// Pairs of lanes (2i, 2i+1).
+__device__ __forceinline__ int pair_sum_i(int v) { return v + dpp_mov_i<0xB1>(v); }
+
+// ---- scalar conversions -----------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __builtin_bit_cast(float, h << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t x = __builtin_bit_cast(uint32_t, f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_act(const void* p, size_t i);
+template <>
+__device__ __forceinline__ float load_act<NVE_DT_F16>(const void* p, size_t i) {
+  return (float)((const _Float16*)p)[i];
+}
+template <>
+__device__ __forceinline__ float load_act<NVE_DT_BF16>(const void* p, size_t i) {
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+template <>
+__device__ __forceinline__ float load_act<NVE_DT_F32>(const void* p, size_t i) {
+  return ((const float*)p)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void store_out(void* p, size_t i, float v);
+template <>
+__device__ __forceinline__ void store_out<NVE_DT_F16>(void* p, size_t i, float v) {
+  ((_Float16*)p)[i] = (_Float16)v;  // round to nearest even
+}
+template <>
+__device__ __forceinline__ void store_out<NVE_DT_BF16>(void* p, size_t i, float v) {
+  ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+}
+template <>
+__device__ __forceinline__ void store_out<NVE_DT_F32>(void* p, size_t i, float v) {
+  ((float*)p)[i] = v;
+}
+
+// Barrier that waits only for this wave's LDS traffic (not for outstanding global
+// loads), so weight loads issued before it stay in flight across the barrier.
+// The fences are scoped to the LDS address space ("local"), so the compiler emits
+// lgkmcnt(0) before s_barrier instead of vmcnt(0).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+}  // namespace nve
+
+// ---- host-side helpers shared by the translation units -----------------------
+namespace nve_host {
+int set_status(int st);  // records the last status, returns st
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+int launch_status();  // hipGetLastError mapped to an NVE status
+}  // namespace nve_host

@@ -1,0 +1,285 @@
+// gemv_w4a8.hip -- W4A8 decode GEMV for gfx950 (int4 weights x int8 activations).
+//
+// Computes, per output row n (cuda/nve_kernels.cu:796-878 restated for CDNA4):
+//   acc[n,b] = sum_{i<32} (nib_i - 8) * xq[32b + i]            exact int32
+//   y[n]     = sum_b ws[n,b] * xs[b] * acc[n,b]                fp32
+//
+// MI355X design:
+//   * Each wave owns R output rows.  Lane l of the wave handles the 32-weight blocks
+//     b = l, l+64, l+128, ... of those rows, so every weight load instruction of the
+//     wave is one contiguous 1 KiB (nibbles, global_load_dwordx4) or 256 B (scales,
+//     global_load_dword) span of HBM: fully coalesced for any K.
+//   * All R x NJ block loads of a wave are issued before any arithmetic (NJ = blocks
+//     per lane), so each lane keeps R*NJ*20 bytes in flight; R is picked so that
+//     R*NJ ~ 8 (160 B/lane, 10 KiB/wave).
+//   * The activation vector is staged once per workgroup in LDS: xq split into two
+//     planes (elements 0-15 and 16-31 of each block, 16 B per block per plane, so a
+//     wave's ds_read_b128 walks consecutive 16 B words without bank conflicts) and a
+//     {sum(xq), xs} pair per block.  The staging loads are issued before the weight
+//     loads and the barrier only waits for LDS traffic, so weight loads stay in
+//     flight across it.
+//   * The block dot product is 8 v_dot4_i32_i8 on the raw nibbles (0..15) with the
+//     -8 offset removed exactly once per block via -8 * sum(xq) (the reference's
+//     bias correction, cuda/nve_kernels.cu:845-853).
+//   * Row sums are finished with a DPP wave reduction (no LDS round trip).
+//   * Up to three weight matrices sharing the same activations (Q/K/V) run in one
+//     launch: workgroups are partitioned into segments, one per matrix.
+#include "common.h"
+#include "w4_launch.h"
+
+namespace nve {
+
+// Exact int32 accumulator of one Q4_0 block (GPU nibble order) against 32 int8
+// activations: lo = elements 0..15, hi = elements 16..31 (4 per dword).
+__device__ __forceinline__ int w4a8_block_dot(uint4 w, int4 lo, int4 hi, int sumq) {
+  const unsigned M = 0x0F0F0F0Fu;
+  int s = 0;
+  s = __builtin_amdgcn_sdot4((int)(w.x & M), lo.x, s, false);
+  s = __builtin_amdgcn_sdot4((int)((w.x >> 4) & M), hi.x, s, false);
+  s = __builtin_amdgcn_sdot4((int)(w.y & M), lo.y, s, false);
+  s = __builtin_amdgcn_sdot4((int)((w.y >> 4) & M), hi.y, s, false);
+  s = __builtin_amdgcn_sdot4((int)(w.z & M), lo.z, s, false);
+  s = __builtin_amdgcn_sdot4((int)((w.z >> 4) & M), hi.z, s, false);
+  s = __builtin_amdgcn_sdot4((int)(w.w & M), lo.w, s, false);
+  s = __builtin_amdgcn_sdot4((int)((w.w >> 4) & M), hi.w, s, false);
+  return s - 8 * sumq;
+}
+
+__device__ __forceinline__ int sum_i8x16(int4 v) {
+  int s = 0;
+  s = __builtin_amdgcn_sdot4(v.x, 0x01010101, s, false);
+  s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
+  s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
+  s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
+  return s;
+}
+
+// LDS layout for K activations (nb = K/32 blocks, plus one spare slot written by
+// threads past the end of the vector):
+//   int4 lo[nb+1]; int4 hi[nb+1]; int2 bs[nb+1] = {sum(xq of block), bits(xs[b])}
+__host__ __device__ constexpr size_t w4a8_lds_bytes(int K) {
+  return (size_t)(K / 32 + 1) * (16 + 16 + 8);
+}
+
+// Stage xq/xs into LDS.  Thread t handles 16-byte chunks i = t + 256*s; chunk i is
+// half (i & 1) of block i >> 1, and lanes 2k / 2k+1 hold the two halves of a block
+// so the per-block sum(xq) is a DPP pair sum.  Loads are unconditional (clamped
+// index) so the compiler can count outstanding loads exactly; only LDS writes are
+// predicated.
+template <int SPT>
+struct W4A8Stage {
+  int4 v[SPT];
+  float xs[SPT];
+};
+
+template <int SPT>
+__device__ __forceinline__ void w4a8_stage_issue(W4A8Stage<SPT>& st, const int8_t* __restrict__ xq,
+                                                 const float* __restrict__ xs, int nchunk) {
+#pragma unroll
+  for (int s = 0; s < SPT; ++s) {
+    const int i = min((int)threadIdx.x + 256 * s, nchunk - 1);
+    st.v[s] = ((const int4*)xq)[i];
+    st.xs[s] = xs[i >> 1];
+  }
+}
+
+__device__ __forceinline__ void w4a8_stage_put(int4 v, float xsb, int i, bool valid, int nb,
+                                               int4* s_lo, int4* s_hi, int2* s_bs) {
+  // Both lanes of a pair write the same {sum, xs} word and each writes its half to
+  // the lo or hi plane by address select: no branches, so no load is sunk.  Lanes
+  // past the end (valid == false) write to the spare slot nb.
+  const int b = valid ? (i >> 1) : nb;
+  const int q = pair_sum_i(sum_i8x16(v));
+  int4* dst = (i & 1) ? s_hi : s_lo;
+  dst[b] = v;
+  s_bs[b] = make_int2(q, __builtin_bit_cast(int, xsb));
+}
+
+template <int SPT>
+__device__ __forceinline__ void w4a8_stage_write(const W4A8Stage<SPT>& st, int4* s_lo, int4* s_hi,
+                                                 int2* s_bs, int nchunk) {
+#pragma unroll
+  for (int s = 0; s < SPT; ++s) {
+    // nchunk is even, so the two lanes of a pair are both valid or both not.
+    const int i = threadIdx.x + 256 * s;
+    w4a8_stage_put(st.v[s], st.xs[s], i, i < nchunk, nchunk >> 1, s_lo, s_hi, s_bs);
+  }
+}
+
+// Staging for K > 16384 (MULTI kernels): loads and LDS writes in one loop.
+__device__ __forceinline__ void w4a8_stage_loop(const int8_t* __restrict__ xq,
+                                                const float* __restrict__ xs, int4* s_lo,
+                                                int4* s_hi, int2* s_bs, int nchunk) {
+  for (int base = 0; base < nchunk; base += 256) {
+    const int i = base + threadIdx.x;
+    const int ic = min(i, nchunk - 1);
+    w4a8_stage_put(((const int4*)xq)[ic], xs[ic >> 1], i, i < nchunk, nchunk >> 1, s_lo, s_hi,
+                   s_bs);
+  }
+}
+
+// R rows per wave, NJ 64-block chunks per lane in registers.  MULTI = K needs more
+// than one pass of NJ chunks (K > 64*NJ*32); then staging runs as a loop.
+template <int OUT_DT, int R, int NJ, bool MULTI>
+__global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict__ xq,
+                                                        const float* __restrict__ xs,
+                                                        W4Segs segs, int K) {
+  constexpr int SPT = (NJ + 1) / 2;  // staging passes: 2*nb <= 128*NJ chunks of 16 B
+  extern __shared__ int4 lds[];
+  const int nb = K >> 5;
+  const int nchunk = 2 * nb;
+  int4* s_lo = lds;
+  int4* s_hi = lds + (nb + 1);
+  int2* s_bs = (int2*)(lds + 2 * (nb + 1));
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  // Segment (matrix) of this workgroup: uniform, resolved with scalar selects.
+  const int wg = blockIdx.x;
+  const int sg = (segs.nseg > 1 && wg >= segs.wg_begin[1]) + (segs.nseg > 2 && wg >= segs.wg_begin[2]);
+  const uint8_t* __restrict__ nib = sg == 0 ? segs.nib[0] : (sg == 1 ? segs.nib[1] : segs.nib[2]);
+  const float* __restrict__ ws = sg == 0 ? segs.sc[0] : (sg == 1 ? segs.sc[1] : segs.sc[2]);
+  void* __restrict__ out = sg == 0 ? segs.out[0] : (sg == 1 ? segs.out[1] : segs.out[2]);
+  const int N = sg == 0 ? segs.n[0] : (sg == 1 ? segs.n[1] : segs.n[2]);
+  const int wg0 = sg == 0 ? 0 : (sg == 1 ? segs.wg_begin[1] : segs.wg_begin[2]);
+  const int row0 = ((wg - wg0) * 4 + wave) * R;
+
+  W4A8Stage<SPT> st;
+  if (!MULTI) w4a8_stage_issue<SPT>(st, xq, xs, nchunk);
+  // Keep the issue order: staging loads, then weight loads, then LDS writes (which
+  // then wait only for the older staging loads).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Weight loads.  Blocks past the end of the row (b >= nb, only in the last chunk
+  // of a row) re-load block nb-1 and are zeroed at use, so no load is predicated.
+  uint4 wv[R][NJ];
+  float wsc[R][NJ];
+  const size_t row_bytes = (size_t)(K >> 1);
+  auto issue = [&](int jb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, N - 1);
+      const uint4* rn = (const uint4*)(nib + (size_t)row * row_bytes);
+      const float* rs = ws + (size_t)row * nb;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int b = jb + lane + 64 * j;
+        const int bb = min(b, nb - 1);
+        wv[r][j] = rn[bb];
+        wsc[r][j] = rs[bb];
+      }
+    }
+  };
+  issue(0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (!MULTI)
+    w4a8_stage_write<SPT>(st, s_lo, s_hi, s_bs, nchunk);
+  else
+    w4a8_stage_loop(xq, xs, s_lo, s_hi, s_bs, nchunk);
+  lds_barrier();
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+  for (int jb = 0;;) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int b = jb + lane + 64 * j;
+      const int bb = min(b, nb - 1);
+      const int4 lo = s_lo[bb];
+      const int4 hi = s_hi[bb];
+      const int2 bs = s_bs[bb];
+      // Lanes past the end of the row contribute nothing.
+      const float xsf = b < nb ? __builtin_bit_cast(float, bs.y) : 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int a = w4a8_block_dot(wv[r][j], lo, hi, bs.x);
+        acc[r] = fmaf(wsc[r][j] * xsf, (float)a, acc[r]);
+      }
+    }
+    if (!MULTI) break;
+    jb += 64 * NJ;
+    if (jb >= nb) break;
+    issue(jb);
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v = wave_sum_to_lane63(acc[r]);
+    if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+  }
+}
+
+// Debug export: exact int32 block accumulators acc[n, b] through w4a8_block_dot.
+__global__ __launch_bounds__(256) void w4a8_block_acc_kernel(const int8_t* __restrict__ xq,
+                                                             const uint8_t* __restrict__ nib,
+                                                             int32_t* __restrict__ acc, int N,
+                                                             int K) {
+  const int nb = K >> 5;
+  const size_t total = (size_t)N * nb;
+  for (size_t t = (size_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (size_t)gridDim.x * 256) {
+    const size_t n = t / nb;
+    const int b = (int)(t % nb);
+    const uint4 w = ((const uint4*)(nib + n * (size_t)(K >> 1)))[b];
+    const int4 lo = ((const int4*)xq)[2 * b];
+    const int4 hi = ((const int4*)xq)[2 * b + 1];
+    acc[t] = w4a8_block_dot(w, lo, hi, sum_i8x16(lo) + sum_i8x16(hi));
+  }
+}
+
+}  // namespace nve
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+namespace nve_host {
+
+template <int OUT_DT, int R, int NJ, bool MULTI>
+static hipError_t launch_w4a8_t(const int8_t* xq, const float* xs, const W4Segs& segs, int K,
+                                int grid, hipStream_t stream) {
+  const size_t lds = nve::w4a8_lds_bytes(K);
+  auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, xq, xs, segs, K);
+  return hipGetLastError();
+}
+
+template <int OUT_DT>
+static hipError_t launch_w4a8_dt(const int8_t* xq, const float* xs, W4Segs segs, int K,
+                                 hipStream_t stream) {
+  const W4Tiling t = choose_w4_tiling(segs, K);
+  finalize_segments(segs, t.R);
+  const int grid = segs.wg_total;
+#define NVE_W4A8_CASE(RR, JJ, MM) \
+  if (t.R == RR && t.NJ == JJ && t.multi == MM) \
+    return launch_w4a8_t<OUT_DT, RR, JJ, MM>(xq, xs, segs, K, grid, stream);
+  NVE_W4_TILING_CASES(NVE_W4A8_CASE)
+#undef NVE_W4A8_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
+                       hipStream_t stream) {
+  switch (out_dt) {
+    case NVE_DT_F16: return launch_w4a8_dt<NVE_DT_F16>(xq, xs, segs, K, stream);
+    case NVE_DT_BF16: return launch_w4a8_dt<NVE_DT_BF16>(xq, xs, segs, K, stream);
+    default: return launch_w4a8_dt<NVE_DT_F32>(xq, xs, segs, K, stream);
+  }
+}
+
+hipError_t launch_w4a8_block_acc(const int8_t* xq, const uint8_t* nib, int32_t* acc, int N, int K,
+                                 hipStream_t stream) {
+  const size_t total = (size_t)N * (K / 32);
+  size_t g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(nve::w4a8_block_acc_kernel, dim3((unsigned)g), dim3(256), 0, stream, xq, nib, acc,
+                     N, K);
+  return hipGetLastError();
+}
+
+}  // namespace nve_host

@@ -1,0 +1,114 @@
+"""The C ABI library loads, exports every symbol include/nve_kernels.h declares, and
+rejects bad arguments with the documented status codes before touching the GPU.
+CPU only (no compute calls)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nve_kernels.h"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nve_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from nve_amd._lib import lib
+    return lib()
+
+
+def test_header_declarations_found():
+    names = _declared()
+    for must in ("nve_quantize_f16_q8", "nve_matvec_w4a8", "nve_matvec_w4a16", "nve_qkv_matvec_w4a16"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(L):
+    missing = [n for n in _declared() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    from nve_amd._lib import SIGNATURES
+    assert sorted(SIGNATURES) == _declared()
+
+
+def test_version_and_status_strings(L):
+    assert b"gfx950" in L.nve_hip_version()
+    assert b"null" in L.nve_hip_status_string(-1)
+    assert b"shape" in L.nve_hip_status_string(-2)
+    assert b"align" in L.nve_hip_status_string(-3)
+
+
+P16 = 0x10000  # an aligned fake device address; validation fails before any use
+
+
+def test_w4a8_argument_errors(L):
+    f = L.nve_hip_matvec_w4a8
+    assert f(None, P16, P16, P16, P16, 2, 8, 64, None) == -1           # null xq
+    assert f(P16, P16, P16, P16, P16, 2, 8, 48, None) == -2            # K % 32
+    assert f(P16, P16, P16, P16, P16, 2, 0, 64, None) == -2            # N = 0
+    assert f(P16, P16, P16, P16, P16, 2, 8, 65536, None) == -5         # K > NVE_MAX_K
+    assert f(P16, P16, P16 + 2, P16, P16, 2, 8, 64, None) == -3        # nibbles not 16B aligned
+    assert f(P16 + 4, P16, P16, P16, P16, 2, 8, 64, None) == -3        # xq not 16B aligned
+    assert f(P16, P16, P16, P16, P16, 7, 8, 64, None) == -4            # out dtype
+    assert L.nve_hip_last_status() == -4
+
+
+def test_w4a16_argument_errors(L):
+    f = L.nve_hip_matvec_w4a16
+    assert f(None, 0, P16, P16, None, P16, 0, 8, 64, None) == -1
+    assert f(P16, 2, P16, P16, None, P16, 0, 8, 64, None) == -4        # f32 x not accepted
+    assert f(P16, 0, P16, P16, P16 + 4, P16, 0, 8, 64, None) == -3     # awq misaligned
+    assert f(P16, 0, P16, P16, None, P16, 0, -1, 64, None) == -2
+
+
+def test_batched_and_prep_argument_errors(L):
+    assert L.nve_hip_matvec_w4a8_batched(0, P16, P16, 0, P16, P16, P16, 2, 8, 64, None) == -2
+    assert L.nve_hip_matvec_w4a8_batched(17, P16, P16, 0, P16, P16, P16, 2, 8, 64, None) == -2
+    assert L.nve_hip_matvec_w4a8_batched(4, P16, P16, 5, P16, P16, P16, 2, 8, 64, None) == -4
+    assert L.nve_hip_quantize_q8(P16, 0, 1, 40, P16, P16, None) == -2
+    assert L.nve_hip_quantize_q8(P16 + 2, 0, 1, 64, P16, P16, None) == -3
+    assert L.nve_hip_quantize_q8_rows(P16, 9, 1, 64, P16, P16, None) == -4
+    assert L.nve_hip_q4_quantize(P16, 2, 4, 33, P16, P16, None) == -2
+    assert L.nve_hip_q4_repack(P16, 4, 64, P16 + 8, P16, None) == -3
+    assert L.nve_hip_w4a8_block_acc(None, P16, P16, 1, 32, None) == -1
+    assert L.nve_hip_stream_read(P16, 24, P16, None) == -2
+    assert L.nve_hip_qkv_matvec_w4a16(P16, 0, P16, P16, None, 8, P16, P16, None, 0, P16, P16, None, 8,
+                                      P16, P16, P16, 0, 64, None) == -2
+
+
+def test_dispatch_env_rules(L, orc, monkeypatch):
+    """nve_use_w4a8 (src/gpu_layer.rs:1013-1025) against the oracle's truth table."""
+    monkeypatch.delenv("NVE_NO_W4A8", raising=False)
+    monkeypatch.delenv("NVE_W4A8_THRESHOLD", raising=False)
+    for imp in (0.0, 0.3, 0.6999, 0.7, 0.71, 1.0):
+        assert L.nve_use_w4a8(imp) == int(orc.use_w4a8(imp, False)), imp
+    monkeypatch.setenv("NVE_W4A8_THRESHOLD", "0.25")
+    for imp in (0.0, 0.2499, 0.25, 0.5):
+        assert L.nve_use_w4a8(imp) == int(orc.use_w4a8(imp, False, 0.25)), imp
+    for bad in ("abc", " 0.25", "0x1p-2", "0.25 ", ""):
+        monkeypatch.setenv("NVE_W4A8_THRESHOLD", bad)  # unparsable -> default 0.7
+        assert L.nve_use_w4a8(0.5) == 1 and L.nve_use_w4a8(0.7) == 0, repr(bad)
+    monkeypatch.setenv("NVE_W4A8_THRESHOLD", "1e-1")
+    assert L.nve_use_w4a8(0.05) == 1 and L.nve_use_w4a8(0.1) == 0
+    monkeypatch.setenv("NVE_NO_W4A8", "1")
+    assert L.nve_use_w4a8(0.0) == 0
+    monkeypatch.setenv("NVE_NO_W4A8", "")  # set but empty still counts as set
+    assert L.nve_use_w4a8(0.0) == 0
+
+
+def test_product_path_has_no_oracle_dependency():
+    """Nothing under nve_amd/ imports or links the oracle."""
+    for p in (ROOT / "nve_amd").rglob("*"):
+        if p.suffix in (".py", ".hip", ".h", ".cpp"):
+            assert "oracle" not in p.read_text(), p
