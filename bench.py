@@ -1,0 +1,403 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized decode GEMV path (W4A8 / W4A16).
+
+Workload: the Llama-3.1-8B layer-shape suite at batch 1 --
+q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096, down 4096x14336,
+lm_head 128256x4096 -- in W4A8 (fp16 activations quantized per 32-group to int8 by
+nve_quantize_f16_q8, int8 x int4 on v_dot4) and in W4A16 (bf16 activations).
+Weights: N(0, 0.02) from a seeded generator, int4 group-quantized on the device by
+the library's Q4_0 quantizer (src/quantize.rs:711-731 semantics).  Activations:
+N(0,1) with 0.5% of channels at +-20 sigma.
+
+One step = one pass over the suite in both precisions (W4A8: 5 activation
+quantizations + 8 GEMVs; W4A16: 8 GEMVs), captured once per weight copy as a HIP
+graph; consecutive steps use different weight copies (>= 1 GB in rotation), so the
+256 MB MALL cannot serve the weights and every byte comes from HBM.
+
+value = algorithmic bytes of one step / measured step time (GB/s), with the
+algorithmic bytes of a GEMV = N*K/2 (nibbles) + N*K/32*4 (f32 scales) + activation
+bytes (W4A8: K + K/32*4, W4A16: 2K) + output bytes.
+
+The roofline object reports the dominant kernel of the step (the W4A8 GEMV at the
+lm_head shape, fp32 logits: the largest single launch; it is the only launch of its
+kernel instantiation in the step) timed on its own in a graph of back-to-back
+launches with HIP events on the stream it runs on.  cpu_baseline times the
+reference's CPU quantized GEMV (QuantizedTensor::matvec_f32 + q4_dot_row_avx2,
+restated in oracle/) on the host cores over a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "W4A8/W4A16 GEMV GB/s & % HBM peak at 8B shapes; decode tok/s (1 GPU)"
+HBM_PEAK_GBS = 8000.0
+
+SUITE_8B = [  # name, N, K
+    ("q_proj", 4096, 4096),
+    ("k_proj", 1024, 4096),
+    ("v_proj", 1024, 4096),
+    ("o_proj", 4096, 4096),
+    ("gate_proj", 14336, 4096),
+    ("up_proj", 14336, 4096),
+    ("down_proj", 4096, 14336),
+    ("lm_head", 128256, 4096),
+]
+
+
+def weight_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * (k // 32) * 4
+
+
+def gemv_bytes(n: int, k: int, prec: str, out_bytes: int) -> int:
+    act = (k + (k // 32) * 4) if prec == "w4a8" else 2 * k
+    return weight_bytes(n, k) + act + n * out_bytes
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+def make_inputs(torch, hk, copies_layer: int, copies_head: int, seed: int = 0x4E5645):
+    """Quantized weight copies for every suite shape (device-side generation)."""
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(seed)
+    weights = {}
+    for name, n, k in SUITE_8B:
+        c = copies_head if name == "lm_head" else copies_layer
+        sets = []
+        for _ in range(c):
+            w = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32).mul_(0.02)
+            nib, sc = hk.q4_quantize(w)
+            del w
+            sets.append((nib, sc))
+        weights[name] = sets
+    torch.cuda.synchronize()
+    return weights
+
+
+def make_activation(torch, k: int, seed: int):
+    import numpy as np
+    r = np.random.default_rng(seed)
+    x = r.standard_normal(k).astype(np.float32)
+    idx = r.choice(k, size=max(1, round(0.005 * k)), replace=False)
+    x[idx] = np.where(r.random(idx.size) < 0.5, -20.0, 20.0)
+    return torch.from_numpy(x).cuda()
+
+
+class Step:
+    """One pass over the suite in both precisions on weight copy `ci`, as raw C-ABI
+    launches into preallocated buffers (capturable)."""
+
+    def __init__(self, torch, lib, weights, acts):
+        self.t = torch
+        self.L = lib
+        self.w = weights
+        self.acts = acts
+        dev = "cuda"
+        self.bufs = {}
+        for name, n, k in SUITE_8B:
+            odt = torch.float32 if name == "lm_head" else torch.float16
+            self.bufs[name] = (torch.empty(n, dtype=odt, device=dev),
+                               torch.empty(n, dtype=torch.float32 if name == "lm_head" else torch.bfloat16,
+                                           device=dev))
+        self.xq = {k: (torch.empty(k, dtype=torch.int8, device=dev), torch.empty(k // 32, dtype=torch.float32,
+                                                                                  device=dev))
+                   for k in (4096, 14336)}
+
+    def _quant(self, x16, k, s):
+        xq, xs = self.xq[k]
+        st = self.L.nve_hip_quantize_q8(x16.data_ptr(), 0, 1, k, xq.data_ptr(), xs.data_ptr(), s)
+        assert st == 0, st
+        return xq, xs
+
+    def w4a8(self, name, ci, xq, xs, s):
+        n, k = [(n, k) for nm, n, k in SUITE_8B if nm == name][0]
+        nib, sc = self.w[name][ci % len(self.w[name])]
+        out = self.bufs[name][0]
+        odt = 2 if out.dtype == self.t.float32 else 0
+        st = self.L.nve_hip_matvec_w4a8(xq.data_ptr(), xs.data_ptr(), nib.data_ptr(), sc.data_ptr(),
+                                        out.data_ptr(), odt, n, k, s)
+        assert st == 0, st
+
+    def w4a16(self, name, ci, xb, s):
+        n, k = [(n, k) for nm, n, k in SUITE_8B if nm == name][0]
+        nib, sc = self.w[name][ci % len(self.w[name])]
+        out = self.bufs[name][1]
+        odt = 2 if out.dtype == self.t.float32 else 1
+        st = self.L.nve_hip_matvec_w4a16(xb.data_ptr(), 1, nib.data_ptr(), sc.data_ptr(), None, out.data_ptr(),
+                                         odt, n, k, s)
+        assert st == 0, st
+
+    def run(self, ci):
+        s = self.t.cuda.current_stream().cuda_stream
+        a = self.acts
+        # W4A8: quantize once for q/k/v (src/gpu_layer.rs:658-661), re-quantize for o,
+        # once for gate/up, again for down, and for the lm_head input.
+        xq, xs = self._quant(a["h16"], 4096, s)
+        for nm in ("q_proj", "k_proj", "v_proj"):
+            self.w4a8(nm, ci, xq, xs, s)
+        xq, xs = self._quant(a["attn16"], 4096, s)
+        self.w4a8("o_proj", ci, xq, xs, s)
+        xq, xs = self._quant(a["h216"], 4096, s)
+        self.w4a8("gate_proj", ci, xq, xs, s)
+        self.w4a8("up_proj", ci, xq, xs, s)
+        xq, xs = self._quant(a["mid16"], 14336, s)
+        self.w4a8("down_proj", ci, xq, xs, s)
+        xq, xs = self._quant(a["final16"], 4096, s)
+        self.w4a8("lm_head", ci, xq, xs, s)
+        # W4A16 (bf16 activations)
+        for nm in ("q_proj", "k_proj", "v_proj"):
+            self.w4a16(nm, ci, a["hb"], s)
+        self.w4a16("o_proj", ci, a["attnb"], s)
+        self.w4a16("gate_proj", ci, a["h2b"], s)
+        self.w4a16("up_proj", ci, a["h2b"], s)
+        self.w4a16("down_proj", ci, a["midb"], s)
+        self.w4a16("lm_head", ci, a["finalb"], s)
+
+    def step_bytes(self) -> int:
+        tot = 0
+        for name, n, k in SUITE_8B:
+            ob = 4 if name == "lm_head" else 2
+            tot += gemv_bytes(n, k, "w4a8", ob) + gemv_bytes(n, k, "w4a16", ob)
+        # activation quantization: read fp16 x, write int8 + f32 scales (5 launches)
+        for k in (4096, 4096, 4096, 14336, 4096):
+            tot += 2 * k + k + (k // 32) * 4
+        return tot
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_graphs(torch, graphs, reps: int) -> float:
+    """Replay `graphs` round-robin `reps` times; returns ms per replay."""
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
+    """Average launch duration of every (shape, precision) GEMV, each timed on its own in
+    a graph of back-to-back launches over rotating weight copies."""
+    rows = {}
+    s_bufs = {}
+    for name, n, k in SUITE_8B:
+        sets = weights[name]
+        for prec in ("w4a8", "w4a16"):
+            odt_t = torch.float32 if name == "lm_head" else (torch.float16 if prec == "w4a8" else torch.bfloat16)
+            out = torch.empty(n, dtype=odt_t, device="cuda")
+            odt = {torch.float32: 2, torch.float16: 0, torch.bfloat16: 1}[odt_t]
+            if prec == "w4a8":
+                xq = torch.empty(k, dtype=torch.int8, device="cuda")
+                xs = torch.empty(k // 32, dtype=torch.float32, device="cuda")
+                x16 = acts["mid16"] if k == 14336 else acts["h16"]
+                assert L.nve_hip_quantize_q8(x16.data_ptr(), 0, 1, k, xq.data_ptr(), xs.data_ptr(), None) == 0
+
+                def body(sets=sets, xq=xq, xs=xs, out=out, odt=odt, n=n, k=k):
+                    s = torch.cuda.current_stream().cuda_stream
+                    for i in range(launches_per_graph):
+                        nib, sc = sets[i % len(sets)]
+                        assert L.nve_hip_matvec_w4a8(xq.data_ptr(), xs.data_ptr(), nib.data_ptr(), sc.data_ptr(),
+                                                     out.data_ptr(), odt, n, k, s) == 0
+            else:
+                xb = acts["midb"] if k == 14336 else acts["hb"]
+
+                def body(sets=sets, xb=xb, out=out, odt=odt, n=n, k=k):
+                    s = torch.cuda.current_stream().cuda_stream
+                    for i in range(launches_per_graph):
+                        nib, sc = sets[i % len(sets)]
+                        assert L.nve_hip_matvec_w4a16(xb.data_ptr(), 1, nib.data_ptr(), sc.data_ptr(), None,
+                                                      out.data_ptr(), odt, n, k, s) == 0
+            body()
+            g = capture(torch, body)
+            time_graphs(torch, [g], 2)
+            reps = 3 if name == "lm_head" else 10
+            ms = time_graphs(torch, [g], reps)
+            us = ms * 1e3 / launches_per_graph
+            ob = 4 if name == "lm_head" else 2
+            b = gemv_bytes(n, k, prec, ob)
+            rows[f"{name}/{prec}"] = {
+                "N": n, "K": k, "us": round(us, 3), "bytes": b,
+                "GBs": round(b / us / 1e3, 1), "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+            }
+            s_bufs[(name, prec)] = (g, out)
+            log(f"  {name:10s} {prec:6s} {us:8.2f} us {b / us / 1e3:8.1f} GB/s {100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}%")
+    return rows
+
+
+def stream_probe(torch, L) -> float:
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1024, device="cuda")
+
+    def body():
+        s = torch.cuda.current_stream().cuda_stream
+        for _ in range(5):
+            assert L.nve_hip_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), s) == 0
+    body()
+    g = capture(torch, body)
+    ms = time_graphs(torch, [g], 3) / 5
+    del buf
+    return buf_gbs(2 << 30, ms)
+
+
+def buf_gbs(nbytes, ms):
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(target_s: float = 12.0) -> dict:
+    """The reference's CPU quantized GEMV (q4_dot_row_avx2 + row-parallel matvec_f32,
+    restated in oracle/) over 8B gate_proj + down_proj, on the host cores."""
+    import numpy as np
+    from oracle import oracle as orc
+    threads = min(16, os.cpu_count() or 1)
+    r = np.random.default_rng(7)
+    mats = []
+    for n, k in ((14336, 4096), (4096, 14336)):
+        w = (r.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+        mats.append((orc.q4_from_f32(w), n, k, r.standard_normal(k).astype(np.float32)))
+        del w
+    b = sum(weight_bytes(n, k) + 4 * k + 4 * n for _, n, k, _ in mats)
+    for data, n, k, x in mats:  # warm
+        orc.q4_matvec_f32(data, n, k, x, threads=threads)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        for data, n, k, x in mats:
+            orc.q4_matvec_f32(data, n, k, x, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    gbs = b * reps / el / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"8B gate_proj 14336x4096 + down_proj 4096x14336, W4 x f32 (QuantizedTensor::matvec_f32 / "
+                      f"q4_dot_row_avx2 restated in oracle/oracle.c), {reps} passes in {el:.1f} s, "
+                      f"{threads} threads; GB/s over the same algorithmic bytes as the GPU"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build's path runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from nve_amd._lib import lib
+    from nve_amd import hip_kernels as hk
+    L = lib()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+
+    # weight copies: layer set 136 MB -> 8 copies (1.09 GB); lm_head 328 MB -> 4 copies
+    copies_layer, copies_head = 8, 4
+    log(f"generating weights ({copies_layer} layer copies, {copies_head} lm_head copies)")
+    weights = make_inputs(torch, hk, copies_layer, copies_head)
+    acts = {}
+    for nm, k, sd in (("h", 4096, 1), ("attn", 4096, 2), ("h2", 4096, 3), ("mid", 14336, 4), ("final", 4096, 5)):
+        x = make_activation(torch, k, sd)
+        acts[nm + "16"] = x.to(torch.float16)
+        acts[nm + "b"] = x.to(torch.bfloat16)
+
+    step = Step(torch, L, weights, acts)
+    n_graphs = max(copies_layer, copies_head)
+    step.run(0)
+    torch.cuda.synchronize()
+    graphs = [capture(torch, lambda ci=ci: step.run(ci)) for ci in range(n_graphs)]
+    time_graphs(torch, graphs, max(args.warmup, 1))
+    ms = time_graphs(torch, graphs, args.steps)
+    sb = step.step_bytes()
+    value = sb / (ms * 1e-3) / 1e9
+    log(f"step: {ms * 1e3:.1f} us, {sb / 1e6:.1f} MB algorithmic, {value:.1f} GB/s")
+
+    log("per-kernel table:")
+    table = kernel_table(torch, L, weights, acts)
+    head = table["lm_head/w4a8"]
+    stream_gbs = stream_probe(torch, L)
+    log(f"HBM streaming probe: {stream_gbs:.1f} GB/s")
+
+    def agg(prec, names):
+        b = sum(table[f"{n}/{prec}"]["bytes"] for n in names)
+        t = sum(table[f"{n}/{prec}"]["us"] for n in names)
+        return round(b / t / 1e3, 1)
+
+    layer_names = [n for n, _, _ in SUITE_8B if n != "lm_head"]
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    traffic = None
+    tf = ROOT / "profiles" / "w4a8_gemv_lm_head_8b_traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 x int8 -> int32 (W4A8); int4 x bf16 -> fp32 (W4A16)",
+        "data": "synthetic (seeded N(0,0.02) weights int4-quantized on device; N(0,1) activations, 0.5% at 20 sigma)",
+        "config": {
+            "workload": "Llama-3.1-8B layer-shape suite, batch 1, W4A8 + W4A16(bf16): q,k,v,o,gate,up,down,lm_head; "
+                        "one step = both precisions over all shapes incl. 5 activation quantizations",
+            "weights_in_rotation_GB": round(sum(weight_bytes(n, k) * len(weights[nm]) for nm, n, k in SUITE_8B) / 1e9, 2),
+            "step_bytes": sb,
+            "graph": "one HIP graph per weight copy, replayed round-robin",
+        },
+        "roofline": {
+            "kernel": "w4a8_gemv_kernel (lm_head 128256x4096, fp32 logits)",
+            "bound": "hbm",
+            "achieved": head["GBs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head["GBs"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": head["bytes"],
+            "us_per_launch": head["us"],
+        },
+        "cpu_baseline": cpu,
+        "suite_8b": table,
+        "suite_8b_aggregate_GBs": {"w4a8_layers": agg("w4a8", layer_names), "w4a16_layers": agg("w4a16", layer_names),
+                                   "w4a8_all": agg("w4a8", [n for n, _, _ in SUITE_8B]),
+                                   "w4a16_all": agg("w4a16", [n for n, _, _ in SUITE_8B])},
+        "hbm_stream_probe_GBs": round(stream_gbs, 1),
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()
