@@ -10,7 +10,8 @@ the library's Q4_0 quantizer (src/quantize.rs:711-731 semantics).  Activations:
 N(0,1) with 0.5% of channels at +-20 sigma.
 
 One step = one pass over the suite in both precisions (W4A8: 5 activation
-quantizations + 8 GEMVs; W4A16: 8 GEMVs), captured once per weight copy as a HIP
+quantizations + 5 GEMV launches, Q/K/V and gate/up each as one grouped launch;
+W4A16: 5 GEMV launches), captured once per weight copy as a HIP
 graph; consecutive steps use different weight copies (>= 1 GB in rotation), so the
 256 MB MALL cannot serve the weights and every byte comes from HBM.
 
@@ -139,29 +140,41 @@ class Step:
                                          odt, n, k, s)
         assert st == 0, st
 
+    def grouped(self, prec, names, ci, x, xs, s):
+        from nve_amd._lib import W4Mat
+        k = [kk for nm, _, kk in SUITE_8B if nm == names[0]][0]
+        arr = (W4Mat * len(names))()
+        for i, name in enumerate(names):
+            n = [nn for nm, nn, _ in SUITE_8B if nm == name][0]
+            nib, sc = self.w[name][ci % len(self.w[name])]
+            out = self.bufs[name][0 if prec == "w4a8" else 1]
+            arr[i] = W4Mat(nib.data_ptr(), sc.data_ptr(), None, out.data_ptr(), n)
+        if prec == "w4a8":
+            st = self.L.nve_hip_grouped_matvec_w4a8(x.data_ptr(), xs.data_ptr(), arr, len(names), 0, k, s)
+        else:
+            st = self.L.nve_hip_grouped_matvec_w4a16(x.data_ptr(), 1, arr, len(names), 1, k, s)
+        assert st == 0, st
+
     def run(self, ci):
         s = self.t.cuda.current_stream().cuda_stream
         a = self.acts
-        # W4A8: quantize once for q/k/v (src/gpu_layer.rs:658-661), re-quantize for o,
-        # once for gate/up, again for down, and for the lm_head input.
+        # W4A8: quantize once for q/k/v (src/gpu_layer.rs:658-661; here one grouped
+        # launch), re-quantize for o, once for gate/up (one grouped launch), again for
+        # down, and for the lm_head input.
         xq, xs = self._quant(a["h16"], 4096, s)
-        for nm in ("q_proj", "k_proj", "v_proj"):
-            self.w4a8(nm, ci, xq, xs, s)
+        self.grouped("w4a8", ("q_proj", "k_proj", "v_proj"), ci, xq, xs, s)
         xq, xs = self._quant(a["attn16"], 4096, s)
         self.w4a8("o_proj", ci, xq, xs, s)
         xq, xs = self._quant(a["h216"], 4096, s)
-        self.w4a8("gate_proj", ci, xq, xs, s)
-        self.w4a8("up_proj", ci, xq, xs, s)
+        self.grouped("w4a8", ("gate_proj", "up_proj"), ci, xq, xs, s)
         xq, xs = self._quant(a["mid16"], 14336, s)
         self.w4a8("down_proj", ci, xq, xs, s)
         xq, xs = self._quant(a["final16"], 4096, s)
         self.w4a8("lm_head", ci, xq, xs, s)
         # W4A16 (bf16 activations)
-        for nm in ("q_proj", "k_proj", "v_proj"):
-            self.w4a16(nm, ci, a["hb"], s)
+        self.grouped("w4a16", ("q_proj", "k_proj", "v_proj"), ci, a["hb"], None, s)
         self.w4a16("o_proj", ci, a["attnb"], s)
-        self.w4a16("gate_proj", ci, a["h2b"], s)
-        self.w4a16("up_proj", ci, a["h2b"], s)
+        self.grouped("w4a16", ("gate_proj", "up_proj"), ci, a["h2b"], None, s)
         self.w4a16("down_proj", ci, a["midb"], s)
         self.w4a16("lm_head", ci, a["finalb"], s)
 
@@ -170,6 +183,8 @@ class Step:
         for name, n, k in SUITE_8B:
             ob = 4 if name == "lm_head" else 2
             tot += gemv_bytes(n, k, "w4a8", ob) + gemv_bytes(n, k, "w4a16", ob)
+        # grouped launches read their shared activation vector once
+        tot -= 3 * ((4096 + 128 * 4) + 2 * 4096)
         # activation quantization: read fp16 x, write int8 + f32 scales (5 launches)
         for k in (4096, 4096, 4096, 14336, 4096):
             tot += 2 * k + k + (k // 32) * 4
@@ -242,6 +257,42 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
             }
             s_bufs[(name, prec)] = (g, out)
             log(f"  {name:10s} {prec:6s} {us:8.2f} us {b / us / 1e3:8.1f} GB/s {100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}%")
+    # grouped launches (one launch for matrices sharing the input)
+    from nve_amd._lib import W4Mat
+    for label, names in (("qkv_grouped", ("q_proj", "k_proj", "v_proj")), ("gate_up_grouped", ("gate_proj", "up_proj"))):
+        k = 4096
+        for prec in ("w4a8", "w4a16"):
+            outs = [torch.empty([n for nm, n, _ in SUITE_8B if nm == x][0], dtype=torch.float16 if prec == "w4a8"
+                                else torch.bfloat16, device="cuda") for x in names]
+            xq = torch.empty(k, dtype=torch.int8, device="cuda")
+            xs = torch.empty(k // 32, dtype=torch.float32, device="cuda")
+            assert L.nve_hip_quantize_q8(acts["h16"].data_ptr(), 0, 1, k, xq.data_ptr(), xs.data_ptr(), None) == 0
+            copies = len(weights[names[0]])
+            arrs = []
+            for ci in range(copies):
+                arr = (W4Mat * len(names))()
+                for i, nm in enumerate(names):
+                    nib, sc = weights[nm][ci]
+                    arr[i] = W4Mat(nib.data_ptr(), sc.data_ptr(), None, outs[i].data_ptr(), outs[i].numel())
+                arrs.append(arr)
+
+            def body(prec=prec, arrs=arrs, xq=xq, xs=xs, names=names):
+                s = torch.cuda.current_stream().cuda_stream
+                for i in range(launches_per_graph):
+                    a = arrs[i % len(arrs)]
+                    if prec == "w4a8":
+                        assert L.nve_hip_grouped_matvec_w4a8(xq.data_ptr(), xs.data_ptr(), a, len(names), 0, k, s) == 0
+                    else:
+                        assert L.nve_hip_grouped_matvec_w4a16(acts["hb"].data_ptr(), 1, a, len(names), 1, k, s) == 0
+            body()
+            g = capture(torch, body)
+            time_graphs(torch, [g], 2)
+            us = time_graphs(torch, [g], 10) * 1e3 / launches_per_graph
+            b = sum(gemv_bytes([n for nm, n, _ in SUITE_8B if nm == x][0], k, prec, 2) for x in names)
+            b -= (len(names) - 1) * ((k + (k // 32) * 4) if prec == "w4a8" else 2 * k)  # one shared input
+            rows[f"{label}/{prec}"] = {"N": sum(o.numel() for o in outs), "K": k, "us": round(us, 3), "bytes": b,
+                                       "GBs": round(b / us / 1e3, 1), "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+            log(f"  {label:15s} {prec:6s} {us:8.2f} us {b / us / 1e3:8.1f} GB/s {100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}%")
     return rows
 
 

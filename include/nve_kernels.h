@@ -108,6 +108,21 @@ int nve_hip_qkv_matvec_w4a8(const int8_t *xq, const float *xq_scales, const uint
                             int Nk, const uint8_t *v_nib, const float *v_sc, int Nv, void *q_out,
                             void *k_out, void *v_out, int out_dtype, int K, void *stream);
 
+/* One weight matrix of a grouped launch (row-major packed W4 in the layout above). */
+typedef struct nve_w4_mat {
+  const uint8_t *nibbles; /* [n, K/2] */
+  const float *scales;    /* [n, K/32] */
+  const float *awq;       /* [K] or NULL (W4A16 only; ignored by W4A8) */
+  void *out;              /* [n] of the call's out_dtype */
+  int n;
+} nve_w4_mat;
+
+/* Grouped W4A8: 1..3 matrices that share K and one quantized activation vector
+ * (Q/K/V, or gate/up of a SwiGLU FFN, src/gpu_layer.rs:936-939) in one launch.
+ * mats is a host array of `count` entries. */
+int nve_hip_grouped_matvec_w4a8(const int8_t *xq, const float *xq_scales, const nve_w4_mat *mats,
+                                int count, int out_dtype, int K, void *stream);
+
 /* Batched W4A8 (small-batch decode, 1 <= M <= NVE_MAX_M).  xq [M,K]; xs_mode
  * NVE_XS_GROUP32_F32: xq_scales f32 [M, K/32]; NVE_XS_ROW_BF16: bf16 [M].
  * out [M, N] of out_dtype.  M >= 4 runs on int8 MFMA; smaller M on v_dot4. */
@@ -126,6 +141,10 @@ int nve_hip_w4a8_block_acc(const int8_t *xq, const uint8_t *nibbles, int32_t *ac
 int nve_hip_matvec_w4a16(const void *x, int x_dtype, const uint8_t *nibbles,
                          const float *scales, const float *awq, void *out, int out_dtype,
                          int N, int K, void *stream);
+
+/* Grouped W4A16: 1..3 matrices sharing K and x in one launch (see the W4A8 twin). */
+int nve_hip_grouped_matvec_w4a16(const void *x, int x_dtype, const nve_w4_mat *mats, int count,
+                                 int out_dtype, int K, void *stream);
 
 /* Twin of nve_qkv_matvec_w4a16 with dtype codes. */
 int nve_hip_qkv_matvec_w4a16(const void *x, int x_dtype, const uint8_t *q_nib,
@@ -155,6 +174,16 @@ int nve_hip_q4_repack(const uint8_t *q4_blocks, int N, int K, uint8_t *nibbles,
 /* Returns 1 (W4A8) when NVE_NO_W4A8 is unset and layer_importance < threshold,
  * where threshold = NVE_W4A8_THRESHOLD parsed as a double, default 0.7; else 0. */
 int nve_use_w4a8(double layer_importance);
+
+/* ---- kernel selection ---------------------------------------------------------- */
+#define NVE_GEMV_AUTO 0       /* persistent kernel when every wave gets >= 2 row tiles */
+#define NVE_GEMV_ONESHOT 1    /* one row tile per wave */
+#define NVE_GEMV_PERSISTENT 2 /* persistent, double-buffered kernel whenever K allows */
+/* Process-wide choice between the two GEMV kernel shapes (both compute bit-identical
+ * results), the persistent grid's workgroups per CU (1..8) and its per-lane buffer
+ * depth in 32-weight blocks (4 or 8); values <= 0 keep the current setting.  Returns
+ * the previous policy.  Not thread-safe; meant for tests and tuning. */
+int nve_hip_set_gemv_policy(int policy, int persistent_wg_per_cu, int persistent_depth);
 
 /* ---- measurement and diagnostics ------------------------------------------ */
 /* Read-only HBM streaming probe: reads `bytes` (multiple of 16, 16-byte aligned)

@@ -20,6 +20,7 @@ NVE_ERR_TOO_LARGE = -5
 DT_F16, DT_BF16, DT_F32 = 0, 1, 2
 XS_GROUP32_F32, XS_ROW_BF16 = 0, 1
 MAX_K = 32768
+GEMV_AUTO, GEMV_ONESHOT, GEMV_PERSISTENT = 0, 1, 2
 MAX_M = 16
 
 _p = C.c_void_p
@@ -35,6 +36,8 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_quantize_q8_rows": (_i, [_p, _i, _i, _i, _p, _p, _p]),
     "nve_hip_matvec_w4a8": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_qkv_matvec_w4a8": (_i, [_p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
+    "nve_hip_grouped_matvec_w4a8": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "nve_hip_grouped_matvec_w4a16": (_i, [_p, _i, _p, _i, _i, _i, _p]),
     "nve_hip_matvec_w4a8_batched": (_i, [_i, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_w4a8_block_acc": (_i, [_p, _p, _p, _i, _i, _p]),
     "nve_hip_matvec_w4a16": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
@@ -43,10 +46,19 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_q4_repack": (_i, [_p, _i, _i, _p, _p, _p]),
     "nve_use_w4a8": (_i, [C.c_double]),
     "nve_hip_stream_read": (_i, [_p, C.c_size_t, _p, _p]),
+    "nve_hip_set_gemv_policy": (_i, [_i, _i, _i]),
     "nve_hip_last_status": (_i, []),
     "nve_hip_status_string": (C.c_char_p, [_i]),
     "nve_hip_version": (C.c_char_p, []),
 }
+
+
+
+class W4Mat(C.Structure):
+    """nve_w4_mat (include/nve_kernels.h)."""
+    _fields_ = [("nibbles", C.c_void_p), ("scales", C.c_void_p), ("awq", C.c_void_p), ("out", C.c_void_p),
+                ("n", C.c_int)]
+
 
 _lib: C.CDLL | None = None
 

@@ -113,29 +113,34 @@ int nve_hip_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t*
   return from_hip(launch_w4a8(xq, xq_scales, s, out_dtype, K, (hipStream_t)stream));
 }
 
+int nve_hip_grouped_matvec_w4a8(const int8_t* xq, const float* xq_scales, const nve_w4_mat* mats,
+                                int count, int out_dtype, int K, void* stream) {
+  if (!xq || !xq_scales || !mats) return set_status(NVE_ERR_NULL);
+  if (count < 1 || count > 3) return set_status(NVE_ERR_SHAPE);
+  if (!dtype_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
+  W4Segs s{};
+  s.nseg = count;
+  for (int i = 0; i < count; ++i) {
+    int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K);
+    if (st != NVE_OK) return set_status(st);
+    if (out_dtype == NVE_DT_F32 && !aligned(mats[i].out, 4)) return set_status(NVE_ERR_ALIGN);
+    s.nib[i] = mats[i].nibbles;
+    s.sc[i] = mats[i].scales;
+    s.out[i] = mats[i].out;
+    s.n[i] = mats[i].n;
+  }
+  if (!aligned(xq, 16) || !aligned(xq_scales, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a8(xq, xq_scales, s, out_dtype, K, (hipStream_t)stream));
+}
+
 int nve_hip_qkv_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t* q_nib,
                             const float* q_sc, int Nq, const uint8_t* k_nib, const float* k_sc,
                             int Nk, const uint8_t* v_nib, const float* v_sc, int Nv, void* q_out,
                             void* k_out, void* v_out, int out_dtype, int K, void* stream) {
-  if (!xq || !xq_scales) return set_status(NVE_ERR_NULL);
-  const uint8_t* nibs[3] = {q_nib, k_nib, v_nib};
-  const float* scs[3] = {q_sc, k_sc, v_sc};
-  void* outs[3] = {q_out, k_out, v_out};
-  const int ns[3] = {Nq, Nk, Nv};
-  W4Segs s{};
-  s.nseg = 3;
-  for (int i = 0; i < 3; ++i) {
-    int st = check_gemv(nibs[i], scs[i], outs[i], ns[i], K);
-    if (st != NVE_OK) return set_status(st);
-    if (out_dtype == NVE_DT_F32 && !aligned(outs[i], 4)) return set_status(NVE_ERR_ALIGN);
-    s.nib[i] = nibs[i];
-    s.sc[i] = scs[i];
-    s.out[i] = outs[i];
-    s.n[i] = ns[i];
-  }
-  if (!dtype_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
-  if (!aligned(xq, 16) || !aligned(xq_scales, 4)) return set_status(NVE_ERR_ALIGN);
-  return from_hip(launch_w4a8(xq, xq_scales, s, out_dtype, K, (hipStream_t)stream));
+  const nve_w4_mat m[3] = {{q_nib, q_sc, nullptr, q_out, Nq},
+                           {k_nib, k_sc, nullptr, k_out, Nk},
+                           {v_nib, v_sc, nullptr, v_out, Nv}};
+  return nve_hip_grouped_matvec_w4a8(xq, xq_scales, m, 3, out_dtype, K, stream);
 }
 
 int nve_hip_w4a8_block_acc(const int8_t* xq, const uint8_t* nibbles, int32_t* acc, int N, int K,
@@ -182,34 +187,38 @@ int nve_hip_matvec_w4a16(const void* x, int x_dtype, const uint8_t* nibbles, con
   return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
 }
 
+int nve_hip_grouped_matvec_w4a16(const void* x, int x_dtype, const nve_w4_mat* mats, int count,
+                                 int out_dtype, int K, void* stream) {
+  if (!x || !mats) return set_status(NVE_ERR_NULL);
+  if (count < 1 || count > 3) return set_status(NVE_ERR_SHAPE);
+  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !dtype_ok(out_dtype))
+    return set_status(NVE_ERR_DTYPE);
+  W4Segs s{};
+  s.nseg = count;
+  for (int i = 0; i < count; ++i) {
+    int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K);
+    if (st != NVE_OK) return set_status(st);
+    if ((mats[i].awq && !aligned(mats[i].awq, 16)) || (out_dtype == NVE_DT_F32 && !aligned(mats[i].out, 4)))
+      return set_status(NVE_ERR_ALIGN);
+    s.nib[i] = mats[i].nibbles;
+    s.sc[i] = mats[i].scales;
+    s.awq[i] = mats[i].awq;
+    s.out[i] = mats[i].out;
+    s.n[i] = mats[i].n;
+  }
+  if (!aligned(x, 16)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
+}
+
 int nve_hip_qkv_matvec_w4a16(const void* x, int x_dtype, const uint8_t* q_nib, const float* q_sc,
                              const float* q_awq, int Nq, const uint8_t* k_nib, const float* k_sc,
                              const float* k_awq, int Nk, const uint8_t* v_nib, const float* v_sc,
                              const float* v_awq, int Nv, void* q_out, void* k_out, void* v_out,
                              int out_dtype, int K, void* stream) {
-  if (!x) return set_status(NVE_ERR_NULL);
-  const uint8_t* nibs[3] = {q_nib, k_nib, v_nib};
-  const float* scs[3] = {q_sc, k_sc, v_sc};
-  const float* awqs[3] = {q_awq, k_awq, v_awq};
-  void* outs[3] = {q_out, k_out, v_out};
-  const int ns[3] = {Nq, Nk, Nv};
-  W4Segs s{};
-  s.nseg = 3;
-  for (int i = 0; i < 3; ++i) {
-    int st = check_gemv(nibs[i], scs[i], outs[i], ns[i], K);
-    if (st != NVE_OK) return set_status(st);
-    if ((awqs[i] && !aligned(awqs[i], 16)) || (out_dtype == NVE_DT_F32 && !aligned(outs[i], 4)))
-      return set_status(NVE_ERR_ALIGN);
-    s.nib[i] = nibs[i];
-    s.sc[i] = scs[i];
-    s.awq[i] = awqs[i];
-    s.out[i] = outs[i];
-    s.n[i] = ns[i];
-  }
-  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !dtype_ok(out_dtype))
-    return set_status(NVE_ERR_DTYPE);
-  if (!aligned(x, 16)) return set_status(NVE_ERR_ALIGN);
-  return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
+  const nve_w4_mat m[3] = {{q_nib, q_sc, q_awq, q_out, Nq},
+                           {k_nib, k_sc, k_awq, k_out, Nk},
+                           {v_nib, v_sc, v_awq, v_out, Nv}};
+  return nve_hip_grouped_matvec_w4a16(x, x_dtype, m, 3, out_dtype, K, stream);
 }
 
 // ---- weight preparation -------------------------------------------------------------
@@ -256,6 +265,15 @@ int nve_use_w4a8(double layer_importance) {
   double parsed;
   if (parse_f64_strict(getenv("NVE_W4A8_THRESHOLD"), &parsed)) threshold = parsed;
   return layer_importance < threshold ? 1 : 0;
+}
+
+// ---- kernel selection ---------------------------------------------------------------
+int nve_hip_set_gemv_policy(int policy, int persistent_wg_per_cu, int persistent_depth) {
+  if (policy != NVE_GEMV_AUTO && policy != NVE_GEMV_ONESHOT && policy != NVE_GEMV_PERSISTENT)
+    return set_status(NVE_ERR_DTYPE);
+  const int prev = gemv_policy();
+  set_gemv_policy(policy, persistent_wg_per_cu, persistent_depth);
+  return prev;
 }
 
 // ---- measurement ----------------------------------------------------------------------

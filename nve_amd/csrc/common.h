@@ -61,6 +61,16 @@ __device__ __forceinline__ float quad_max_f(float v) {
 // Pairs of lanes (2i, 2i+1).
 __device__ __forceinline__ int pair_sum_i(int v) { return v + dpp_mov_i<0xB1>(v); }
 
+// ---- streaming loads ----------------------------------------------------------
+// Weights are read exactly once per GEMV: load them with the nontemporal hint (nt),
+// which keeps the streamed bytes from displacing reusable lines in L2 / MALL.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
+
 // ---- scalar conversions -----------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __builtin_bit_cast(float, h << 16);

@@ -178,26 +178,24 @@ __global__ __launch_bounds__(256) void q4_repack_kernel(const uint8_t* __restric
 }
 
 // ---- HBM streaming probe --------------------------------------------------------
-// Each thread reads 8 x 16 B per iteration (grid-stride), xors into a register and
-// writes one word per workgroup so the loads cannot be removed.
+// Each wave reads 8 contiguous 1 KiB spans (lane l: 16 B at span*1024 + 16*l) with
+// nontemporal loads, xors them and writes one word only on an impossible value, so
+// the loads cannot be removed.  One launch covers the buffer once.
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ buf, size_t n16,
                                                           float* __restrict__ sink) {
+  const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  uint4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    size_t i = (wave * 8 + j) * 64 + lane;
+    if (i >= n16) i = n16 - 1;
+    v[j] = ld_stream(buf + i);
+  }
   uint32_t a = 0;
-  const size_t stride = (size_t)gridDim.x * 256;
-  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  for (; i + 7 * stride < n16; i += 8 * stride) {
-    uint4 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = buf[i + u * stride];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) a ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  }
-  for (; i < n16; i += stride) {
-    const uint4 v = buf[i];
-    a ^= v.x ^ v.y ^ v.z ^ v.w;
-  }
-  a = (uint32_t)__builtin_amdgcn_readfirstlane((int)a) ^ (uint32_t)__builtin_amdgcn_readlane((int)a, 63);
-  if (threadIdx.x == 0 && a == 0x12345678u) sink[blockIdx.x & 1023] = 1.0f;
+  for (int j = 0; j < 8; ++j) a ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  if (a == 0x12345678u) sink[blockIdx.x & 1023] = 1.0f;
 }
 
 }  // namespace nve
@@ -248,7 +246,9 @@ hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, flo
 }
 
 hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream) {
-  hipLaunchKernelGGL(nve::stream_read_kernel, dim3(2048), dim3(256), 0, stream, (const uint4*)buf, bytes / 16, sink);
+  const size_t n16 = bytes / 16;
+  const size_t grid = (n16 + 2047) / 2048;  // 4 waves x 8 spans x 64 lanes per workgroup
+  hipLaunchKernelGGL(nve::stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, stream, (const uint4*)buf, n16, sink);
   return hipGetLastError();
 }
 

@@ -12,9 +12,12 @@ struct W4Segs {
   const float* awq[3];
   void* out[3];
   int n[3];
-  int wg_begin[3];
+  int wg_begin[3];    // one-shot kernels: first workgroup of each matrix
   int nseg;
   int wg_total;
+  int tile_begin[4];  // persistent kernels: first R-row tile of each matrix (+ end)
+  int tiles_total;
+  int wave_begin[4];  // persistent kernels: first wave of each matrix (+ end)
 };
 
 struct W4Tiling {
@@ -53,7 +56,113 @@ inline void finalize_segments(W4Segs& s, int R) {
   X(1, 2, false) X(2, 3, false) X(1, 3, false) X(2, 4, false) X(1, 4, false) X(1, 5, false) \
   X(1, 6, false) X(1, 7, false) X(1, 8, false) X(1, 8, true)
 
+// Persistent kernels: R*NJ ~ depth (4 or 8) blocks per lane per buffer, two buffers.
+inline W4Tiling choose_persistent_tiling(int K, int depth) {
+  const int nb = K / 32;
+  const int nj = (nb + 63) / 64;
+  int r;
+  if (depth >= 8)
+    r = nj == 1 ? 8 : (nj == 2 ? 4 : (nj <= 4 ? 2 : 1));
+  else
+    r = nj == 1 ? 4 : (nj == 2 ? 2 : 1);
+  return W4Tiling{r, nj, false};
+}
+
+inline void finalize_tiles(W4Segs& s, int R) {
+  int t = 0;
+  for (int i = 0; i < 4; ++i) {
+    s.tile_begin[i] = t;
+    if (i < s.nseg) t += (s.n[i] + R - 1) / R;
+  }
+  s.tiles_total = t;
+}
+
+// Split `waves` between the matrices in proportion to their tiles (at least one wave
+// each, never more waves than tiles); returns the number of waves actually used.
+inline int assign_waves(W4Segs& s, int waves) {
+  int used = 0;
+  for (int i = 0; i < 4; ++i) {
+    s.wave_begin[i] = used;
+    if (i < s.nseg) {
+      const int ti = s.tile_begin[i + 1] - s.tile_begin[i];
+      long w = ((long)waves * ti + s.tiles_total - 1) / s.tiles_total;
+      if (w < 1) w = 1;
+      if (w > ti) w = ti;
+      used += (int)w;
+    }
+  }
+  return used;
+}
+
+// The rows of one wave all come from one matrix: the host splits the grid's waves
+// between the matrices of a grouped launch in proportion to their tile counts
+// (W4Segs::wave_begin), so the segment lookup happens once per wave, outside the
+// tile loop, and the loop itself is pure scalar arithmetic on an SGPR tile index.
+struct W4Wave {
+  const uint8_t* nib;
+  const float* ws;
+  void* out;
+  int n;
+  int t0;      // first tile of this wave within its matrix
+  int stride;  // waves assigned to the matrix
+  int tiles;   // tiles of the matrix
+};
+
+// Waves past the last assigned one (the grid is a whole number of 4-wave workgroups)
+// are idle: they map onto wave 0's matrix with no tiles, so their one unconditional
+// prefetch reads tile 0 of a real matrix and nothing else runs.  Segments >= nseg
+// have wave_begin == wave_begin[nseg], so no active wave can select them.
+__host__ __device__ inline W4Wave resolve_wave(const W4Segs& g, int w) {
+  const int wtot = g.wave_begin[g.nseg];
+  const bool idle = w >= wtot;
+  const int wc = idle ? 0 : w;
+  const int sg = wc >= g.wave_begin[2] ? 2 : (wc >= g.wave_begin[1] ? 1 : 0);
+  W4Wave r;
+  r.nib = g.nib[sg];
+  r.ws = g.sc[sg];
+  r.out = g.out[sg];
+  r.n = g.n[sg];
+  r.t0 = wc - g.wave_begin[sg];
+  r.stride = g.wave_begin[sg + 1] - g.wave_begin[sg];
+  r.tiles = idle ? 0 : g.tile_begin[sg + 1] - g.tile_begin[sg];
+  return r;
+}
+
+// Persistent tile results parked per wave in LDS (see w4_persistent.h).
+constexpr int kPersistentMaxTilesPerWave = 8;
+
+// Grid plan of a persistent launch: fills tile_begin / wave_begin and returns the
+// number of 4-wave workgroups (0 if the shape cannot be planned within the per-wave
+// tile limit).  Wave w of the grid runs tiles t0, t0+stride, ... of its matrix.
+inline int plan_persistent(W4Segs& s, int R, int waves_wanted) {
+  finalize_tiles(s, R);
+  int waves = waves_wanted;
+  const int min_waves = (s.tiles_total + kPersistentMaxTilesPerWave - 1) / kPersistentMaxTilesPerWave + s.nseg;
+  if (waves < min_waves) waves = min_waves;
+  waves = assign_waves(s, waves);
+  for (int i = 0; i < s.nseg; ++i) {
+    const int ti = s.tile_begin[i + 1] - s.tile_begin[i];
+    const int wi = s.wave_begin[i + 1] - s.wave_begin[i];
+    if (wi < 1 || (ti + wi - 1) / wi > kPersistentMaxTilesPerWave) return 0;
+  }
+  return (waves + 3) / 4;
+}
+
+#define NVE_W4_PERSISTENT_CASES(X) \
+  X(8, 1) X(4, 1) X(4, 2) X(2, 2) X(2, 3) X(1, 3) X(2, 4) X(1, 4) X(1, 5) X(1, 6) X(1, 7) X(1, 8)
+
 namespace nve_host {
+// Workgroups per CU for the persistent kernels (NVE_PERSISTENT_OCC overrides; 0 turns
+// the persistent kernels off).
+int persistent_occupancy();
+int persistent_depth();
+int gemv_policy();
+void set_gemv_policy(int policy, int occ, int depth);
+bool use_persistent(const W4Segs& s, int K, bool w4a16);
+hipError_t launch_w4a8_persistent(const int8_t* xq, const float* xs, W4Segs segs, int out_dt, int K,
+                                  hipStream_t stream);
+hipError_t launch_w4a16_persistent(const void* x, int x_dt, W4Segs segs, int out_dt, int K,
+                                   hipStream_t stream);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);
 hipError_t launch_w4a8_block_acc(const int8_t* xq, const uint8_t* nib, int32_t* acc, int N, int K,
