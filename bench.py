@@ -346,6 +346,38 @@ def cpu_baseline(target_s: float = 12.0) -> dict:
                       f"{threads} threads; GB/s over the same algorithmic bytes as the GPU"}
 
 
+def traffic_probe(torch, L, hk):
+    """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
+    256 MiB (calibration: 256 MiB read + 256 MiB written), then 5 launches of the
+    roofline kernel (W4A8 GEMV, lm_head 128256x4096, fp32 logits) on 5 distinct weight
+    copies.  Prints the launch order so per-dispatch counters can be matched."""
+    g = torch.Generator(device="cuda").manual_seed(11)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.random_(generator=g)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    n, k = 128256, 4096
+    sets = []
+    for _ in range(5):
+        w = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+        sets.append(hk.q4_quantize(w))
+        del w
+    x16 = make_activation(torch, k, 5).to(torch.float16)
+    xq, xs = hk.quantize_f16_q8(x16)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for nib, sc in sets:
+        assert L.nve_hip_matvec_w4a8(xq.data_ptr(), xs.data_ptr(), nib.data_ptr(), sc.data_ptr(), out.data_ptr(),
+                                     2, n, k, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "traffic", "copy_bytes": 256 << 20, "gemv_bytes_per_launch": gemv_bytes(n, k, "w4a8", 4),
+                      "gemv_launches": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -353,6 +385,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no bench line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -365,6 +399,9 @@ def main():
     L = lib()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.traffic_probe:
+        traffic_probe(torch, L, hk)
+        return
 
     # weight copies: layer set 136 MB -> 8 copies (1.09 GB); lm_head 328 MB -> 4 copies
     copies_layer, copies_head = 8, 4
@@ -401,13 +438,16 @@ def main():
     layer_names = [n for n, _, _ in SUITE_8B if n != "lm_head"]
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
+    # HBM bytes per launch of the roofline kernel, from the calibrated rocprofv3
+    # FETCH_SIZE / WRITE_SIZE passes over `bench.py --traffic-probe` (recorded in
+    # profiles/w4a8_gemv_lm_head_8b_traffic.md)
     traffic = None
-    tf = ROOT / "profiles" / "w4a8_gemv_lm_head_8b_traffic.json"
+    tf = ROOT / "profiles" / "w4a8_gemv_lm_head_8b_traffic.md"
     if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+        import re
+        m = re.search(r"```json\n(.*?)\n```", tf.read_text(), re.S)
+        if m:
+            traffic = json.loads(m.group(1)).get("hbm_bytes_per_launch")
 
     rec = {
         "metric": METRIC,
