@@ -296,6 +296,49 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
     return rows
 
 
+def batched_sweep(torch, L, weights, launches_per_graph: int = 40):
+    """W4A8 at M in {1,2,4,8,16} activation rows (per-row absmax
+    int8, bf16 scales) on the 8B gate (14336x4096) and down (4096x14336) shapes.
+    M >= 4 runs on int8 MFMA (v_mfma_i32_16x16x32_i8, 16 activation columns per
+    instruction, so the issued MFMA work is 2*16*N*K per launch whatever M is)."""
+    import numpy as np
+    rows = {}
+    for name in ("gate_proj", "down_proj"):
+        n, k = [(nn, kk) for nm, nn, kk in SUITE_8B if nm == name][0]
+        sets = weights[name]
+        for m in (1, 2, 4, 8, 16):
+            r = np.random.default_rng(100 + m)
+            x = torch.from_numpy(r.standard_normal((m, k)).astype(np.float32)).cuda().to(torch.bfloat16)
+            xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+            xs = torch.empty(m, dtype=torch.bfloat16, device="cuda")
+            assert L.nve_hip_quantize_q8_rows(x.data_ptr(), 1, m, k, xq.data_ptr(), xs.data_ptr(), None) == 0
+            out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+
+            def body(sets=sets, xq=xq, xs=xs, out=out, m=m, n=n, k=k):
+                s = torch.cuda.current_stream().cuda_stream
+                for i in range(launches_per_graph):
+                    nib, sc = sets[i % len(sets)]
+                    assert L.nve_hip_matvec_w4a8_batched(m, xq.data_ptr(), xs.data_ptr(), 1, nib.data_ptr(),
+                                                         sc.data_ptr(), out.data_ptr(), 0, n, k, s) == 0
+            body()
+            g = capture(torch, body)
+            time_graphs(torch, [g], 2)
+            us = time_graphs(torch, [g], 10) * 1e3 / launches_per_graph
+            b = weight_bytes(n, k) + m * (k + 2) + m * n * 2
+            rec = {"M": m, "N": n, "K": k, "us": round(us, 3), "GBs": round(b / us / 1e3, 1),
+                   "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                   "useful_int8_TOPs": round(2 * m * n * k / us / 1e6, 2),
+                   "kernel": "mfma_i32_16x16x32_i8" if m >= 4 else "v_dot4"}
+            if m >= 4:
+                issued = 2 * 16 * n * k / us / 1e6
+                rec["issued_mfma_TOPs"] = round(issued, 2)
+                rec["mfma_util_vs_5000_TOPs"] = round(issued / 5000.0, 4)
+            rows[f"{name}/M{m}"] = rec
+            log(f"  {name:10s} M={m:2d} {us:8.2f} us {b / us / 1e3:8.1f} GB/s {100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}%"
+                f"  {rec['kernel']}")
+    return rows
+
+
 def stream_probe(torch, L) -> float:
     buf = torch.empty(2 << 30, dtype=torch.uint8, device="cuda")
     sink = torch.zeros(1024, device="cuda")
@@ -427,6 +470,8 @@ def main():
     log("per-kernel table:")
     table = kernel_table(torch, L, weights, acts)
     head = table["lm_head/w4a8"]
+    log("batched W4A8 sweep (per-token int8 activations):")
+    sweep = batched_sweep(torch, L, weights)
     stream_gbs = stream_probe(torch, L)
     log(f"HBM streaming probe: {stream_gbs:.1f} GB/s")
 
@@ -486,6 +531,7 @@ def main():
                                    "w4a8_all": agg("w4a8", [n for n, _, _ in SUITE_8B]),
                                    "w4a16_all": agg("w4a16", [n for n, _, _ in SUITE_8B])},
         "hbm_stream_probe_GBs": round(stream_gbs, 1),
+        "batched_w4a8_8b": sweep,
     }
     print(json.dumps(rec), flush=True)
 

@@ -359,3 +359,25 @@ def test_dispatch_project(orc, torch_dev, hk, monkeypatch):
     q, s = orc.quantize_q8_group(x)
     assert rel_err_floor(y8, orc.matvec_w4a8_f64(q, s, nib, sc, n, k)) <= TOL_W4A8
     assert rel_err_floor(y16, orc.matvec_w4a16_f64(x, nib, sc, n, k)) <= TOL_W4A16
+
+
+@pytest.mark.parametrize("m", [4, 5, 8, 13, 16])
+@pytest.mark.parametrize("n,k", [(16, 32), (17, 96), (300, 160), (1000, 2048), (8200, 4096), (70, 14336),
+                                 (4096, 14336)])
+@pytest.mark.parametrize("per_token", [False, True])
+def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
+    """M >= 4 runs on the int8 MFMA kernel: ragged N, K with a partial last block quad,
+    both wave splits (N/16 below and above 512 tiles)."""
+    torch = torch_dev
+    _, _, nib, ws = _problem(orc, n, k, seed=m * 7 + n)
+    x = to_bf16(activations(k, seed=300 + m, m=m))
+    xq, xs = hk.quantize_q8_rows(up(torch, x).to(torch.bfloat16), per_token=per_token)
+    y = down(hk.matvec_w4a8_batched(xq, xs, up(torch, nib), up(torch, ws), n, k, out_dtype=torch.float32))
+    for r in range(m):
+        if per_token:
+            q, s = orc.quantize_q8_rows_bf16(x[r])
+            ref = orc.matvec_w4a8_f64(q[0], orc.bf16_bits_to_f32(s), nib, ws, n, k, xs_mode=1)
+        else:
+            q, s = orc.quantize_q8_group(x[r])
+            ref = orc.matvec_w4a8_f64(q, s, nib, ws, n, k)
+        assert rel_err_floor(y[r], ref) <= TOL_W4A8, r
