@@ -389,6 +389,64 @@ def cpu_baseline(target_s: float = 12.0) -> dict:
                       f"{threads} threads; GB/s over the same algorithmic bytes as the GPU"}
 
 
+def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool) -> dict:
+    """synthetic Llama-3.2-3B decode at batch 1, greedy.  28 layers
+    (a seeded 30% = 8 W4A16, 20 W4A8; W4A8 lm_head), 512 prefilled N(0,1) bf16 KV
+    positions, one HIP graph per token (all layers + head, position device-resident),
+    `tokens` greedy tokens timed with HIP events on the replay stream.  The CPU leg runs
+    the reference's CPU decode path (Q4 x f32 matvec_f32, AVX2 restated in oracle/, all
+    projections; f32 attention) on the same weights for `cpu_tokens` tokens."""
+    from nve_amd.decode import LLAMA_3_2_3B, DecodeModel
+    s = LLAMA_3_2_3B
+    prefill, max_seq = 512, 1024
+    tokens = min(tokens, max_seq - prefill - warm - 1)
+    m = DecodeModel(s, max_seq=max_seq, prefill=prefill)
+    m.capture()
+    m.start(1)
+    m.generate(warm)
+    torch.cuda.synchronize()
+    m.start(1)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    m.generate(tokens)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / tokens
+    wb = m.step_bytes()
+    kvb = m.kv_bytes(prefill + tokens // 2)  # mean cache length over the timed tokens
+    tok_s = 1e3 / ms
+    n16 = sum(1 for u in m.use_w4a8 if not u)
+    rec = {"tok_per_s": round(tok_s, 1), "ms_per_token": round(ms, 4), "tokens": tokens, "warmup": warm,
+           "layers_w4a8": s.layers - n16, "layers_w4a16": n16, "kv_prefill": prefill,
+           "bytes_per_token": wb + kvb,
+           "GBs": round((wb + kvb) / (ms * 1e-3) / 1e9, 1),
+           "frac_hbm_peak": round((wb + kvb) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "launches_per_token": None}
+    log(f"decode 3B: {ms * 1e3:.1f} us/token, {tok_s:.1f} tok/s, {rec['GBs']} GB/s")
+    if not no_cpu:
+        import numpy as np
+        from oracle import decode_ref as dr
+        log("decode 3B CPU leg: copying weights to host")
+        hm = dr.HostModel(m, with_cpu_blocks=True)
+        threads = min(16, os.cpu_count() or 1)
+        h = hm.embed[1].copy()
+        h, _ = dr.reference_step(hm, h, prefill, threads)  # warm
+        t0 = time.perf_counter()
+        for i in range(cpu_tokens):
+            h, _ = dr.reference_step(hm, h, prefill + 1 + i, threads)
+        el = time.perf_counter() - t0
+        rec["cpu_baseline"] = {"value": round(cpu_tokens / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+                               "sample": f"{cpu_tokens} greedy tokens (after 1 warm) of the same 3B model on the "
+                                         f"reference CPU decode path (QuantizedTensor::matvec_f32 / q4_dot_row_avx2 "
+                                         f"restated in oracle/, f32 activations), {el:.1f} s"}
+        log(f"decode 3B CPU: {cpu_tokens / el:.2f} tok/s on {threads} threads")
+        del hm
+    del m
+    torch.cuda.empty_cache()
+    return rec
+
+
 def traffic_probe(torch, L, hk):
     """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
     256 MiB (calibration: 256 MiB read + 256 MiB written), then 5 launches of the
@@ -428,6 +486,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--cpu-decode-tokens", type=int, default=3)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the 3B decode measurement (for profiling; no bench line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no bench line)")
     args = ap.parse_args()
@@ -444,6 +507,9 @@ def main():
     torch.cuda.set_device(0)
     if args.traffic_probe:
         traffic_probe(torch, L, hk)
+        return
+    if args.decode_only:
+        print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True)}))
         return
 
     # weight copies: layer set 136 MB -> 8 copies (1.09 GB); lm_head 328 MB -> 4 copies
@@ -481,6 +547,11 @@ def main():
         return round(b / t / 1e3, 1)
 
     layer_names = [n for n, _, _ in SUITE_8B if n != "lm_head"]
+    rot_gb = round(sum(weight_bytes(n, k) * len(weights[nm]) for nm, n, k in SUITE_8B) / 1e9, 2)
+    del weights, step, graphs
+    torch.cuda.empty_cache()
+    decode = None if args.no_decode else decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens,
+                                                   args.no_cpu)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     # HBM bytes per launch of the roofline kernel, from the calibrated rocprofv3
@@ -510,7 +581,7 @@ def main():
         "config": {
             "workload": "Llama-3.1-8B layer-shape suite, batch 1, W4A8 + W4A16(bf16): q,k,v,o,gate,up,down,lm_head; "
                         "one step = both precisions over all shapes incl. 5 activation quantizations",
-            "weights_in_rotation_GB": round(sum(weight_bytes(n, k) * len(weights[nm]) for nm, n, k in SUITE_8B) / 1e9, 2),
+            "weights_in_rotation_GB": rot_gb,
             "step_bytes": sb,
             "graph": "one HIP graph per weight copy, replayed round-robin",
         },
@@ -532,6 +603,7 @@ def main():
                                    "w4a16_all": agg("w4a16", [n for n, _, _ in SUITE_8B])},
         "hbm_stream_probe_GBs": round(stream_gbs, 1),
         "batched_w4a8_8b": sweep,
+        "decode_3b": decode,
     }
     print(json.dumps(rec), flush=True)
 

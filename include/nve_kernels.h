@@ -41,6 +41,7 @@ extern "C" {
 #define NVE_DT_F16 0
 #define NVE_DT_BF16 1
 #define NVE_DT_F32 2
+#define NVE_DT_F32_ACCUM 3 /* GEMV output mode only: fp32 out[n] += y (residual add) */
 
 /* ---- activation-scale modes for the W4A8 kernels ------------------------- */
 #define NVE_XS_GROUP32_F32 0 /* one f32 scale per 32 activations (reference mode) */
@@ -95,7 +96,9 @@ int nve_hip_quantize_q8_rows(const void *x, int x_dtype, int M, int K, int8_t *x
                              uint16_t *scales_bf16, void *stream);
 
 /* Twin of nve_matvec_w4a8 with a selectable output dtype (F16, BF16 or F32; the
- * F32 output is the value before any rounding to 16 bits). */
+ * F32 output is the value before any rounding to 16 bits; F32_ACCUM adds the fp32
+ * value into out, which fuses a residual add into the GEMV).  The same output codes
+ * apply to every GEMV entry point below except the batched one. */
 int nve_hip_matvec_w4a8(const int8_t *xq, const float *xq_scales, const uint8_t *nibbles,
                         const float *wt_scales, void *out, int out_dtype, int N, int K,
                         void *stream);
@@ -184,6 +187,80 @@ int nve_use_w4a8(double layer_importance);
  * depth in 32-weight blocks (4 or 8); values <= 0 keep the current setting.  Returns
  * the previous policy.  Not thread-safe; meant for tests and tuning. */
 int nve_hip_set_gemv_policy(int policy, int persistent_wg_per_cu, int persistent_depth);
+
+/* ---- decode step (Llama-style decoder layer around the GEMV path) --------------
+ * Restates gpu_layer_forward_decode (src/gpu_layer.rs:1005-1084) for one token:
+ *   h += o_proj(attn(rope(q), rope(k) ++ K cache, V cache))    with x = rmsnorm(h)
+ *   h += down(silu(gate(x2)) * up(x2))                         with x2 = rmsnorm(h)
+ * Precision per layer: W4A8 (RMSNorm / SiLU-mul quantize their outputs to int8
+ * with group-32 scales, nve_quantize_f16_q8 semantics) or W4A16 (bf16 activations).
+ * Q/K/V and gate/up are single grouped launches; residual adds are fused into the
+ * o_proj / down GEMVs (NVE_DT_F32_ACCUM).  The position of the token is read from
+ * device memory (*pos), so a whole step can be captured in a HIP graph and replayed.
+ * RMSNorm accumulates in f64 (src/ops.rs:12-30); RoPE pairs (i, i+D/2) with
+ * caller-provided cos/sin tables [max_seq, D/2] (src/ops.rs:264-276); attention is
+ * GQA with scale 1/sqrt(D) (src/attention.rs:149-228); the KV cache is bf16. */
+typedef struct nve_decode_config {
+  int hidden;       /* H, multiple of 32 */
+  int num_heads;    /* query heads */
+  int num_kv_heads; /* key/value heads (num_heads / num_kv_heads <= 8) */
+  int head_dim;     /* D: 64, 128 or 256 */
+  int ffn;          /* F, multiple of 32 */
+  int max_seq;      /* KV-cache capacity (positions): <= 16384 (8192 for D = 256) */
+  int vocab;        /* lm_head rows (0 if the workspace is not used by the head) */
+  float eps;        /* RMSNorm epsilon */
+} nve_decode_config;
+
+typedef struct nve_w4_weight {
+  const uint8_t *nibbles; /* [n, k/2], GPU nibble order */
+  const float *scales;    /* [n, k/32] */
+  int n;
+  int k;
+} nve_w4_weight;
+
+typedef struct nve_layer_weights {
+  const uint16_t *input_norm;     /* bf16 [H] */
+  const uint16_t *post_attn_norm; /* bf16 [H] */
+  nve_w4_weight q, k, v, o, gate, up, down;
+} nve_layer_weights;
+
+typedef struct nve_decode_io {
+  float *hidden;          /* fp32 [H] residual stream, updated in place */
+  uint16_t *k_cache;      /* bf16 [num_kv_heads, max_seq, D] of this layer */
+  uint16_t *v_cache;      /* bf16 [num_kv_heads, max_seq, D] */
+  const int *pos;         /* device int: position of this token (< max_seq) */
+  const float *rope_cos;  /* f32 [max_seq, D/2] */
+  const float *rope_sin;  /* f32 [max_seq, D/2] */
+  void *workspace;        /* nve_hip_decode_workspace_bytes() bytes, 256-byte aligned,
+                             zero-filled once after allocation (it holds arrival
+                             counters that every call leaves at zero); one workspace
+                             per stream: calls sharing one must not overlap */
+} nve_decode_io;
+
+typedef struct nve_decode_head {
+  float *hidden;              /* fp32 [H]: final residual in; embedding of the chosen token out */
+  const uint16_t *final_norm; /* bf16 [H] */
+  nve_w4_weight lm_head;      /* [vocab, H] */
+  const uint16_t *embed;      /* bf16 [vocab, H] token embeddings */
+  float *logits;              /* fp32 [vocab] or NULL (workspace) */
+  int *token_out;             /* device int: greedy token (first maximum, src/ops.rs:485-495) */
+  int *pos;                   /* device int, incremented after the step */
+  void *workspace;
+} nve_decode_head;
+
+/* Size of the decode workspace shared by the layer and head calls of one model. */
+size_t nve_hip_decode_workspace_bytes(const nve_decode_config *cfg);
+/* One decoder layer for one token; use_w4a8 selects the layer's precision (see
+ * nve_use_w4a8). */
+int nve_hip_layer_forward_decode(const nve_decode_config *cfg, const nve_layer_weights *w,
+                                 const nve_decode_io *io, int use_w4a8, void *stream);
+/* Final RMSNorm, lm_head GEMV (fp32 logits), greedy argmax, embedding of the chosen
+ * token into hidden, *pos += 1. */
+int nve_hip_decode_head(const nve_decode_config *cfg, const nve_decode_head *head, int use_w4a8,
+                        void *stream);
+/* hidden = embed[*token] (bf16 -> fp32). */
+int nve_hip_embed(const uint16_t *embed, const int *token, float *hidden, int hidden_size,
+                  void *stream);
 
 /* ---- measurement and diagnostics ------------------------------------------ */
 /* Read-only HBM streaming probe: reads `bytes` (multiple of 16, 16-byte aligned)

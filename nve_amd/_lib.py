@@ -17,7 +17,7 @@ NVE_ERR_SHAPE = -2
 NVE_ERR_ALIGN = -3
 NVE_ERR_DTYPE = -4
 NVE_ERR_TOO_LARGE = -5
-DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+DT_F16, DT_BF16, DT_F32, DT_F32_ACCUM = 0, 1, 2, 3
 XS_GROUP32_F32, XS_ROW_BF16 = 0, 1
 MAX_K = 32768
 GEMV_AUTO, GEMV_ONESHOT, GEMV_PERSISTENT = 0, 1, 2
@@ -47,6 +47,10 @@ SIGNATURES: dict[str, tuple] = {
     "nve_use_w4a8": (_i, [C.c_double]),
     "nve_hip_stream_read": (_i, [_p, C.c_size_t, _p, _p]),
     "nve_hip_set_gemv_policy": (_i, [_i, _i, _i]),
+    "nve_hip_decode_workspace_bytes": (C.c_size_t, [_p]),
+    "nve_hip_layer_forward_decode": (_i, [_p, _p, _p, _i, _p]),
+    "nve_hip_decode_head": (_i, [_p, _p, _i, _p]),
+    "nve_hip_embed": (_i, [_p, _p, _p, _i, _p]),
     "nve_hip_last_status": (_i, []),
     "nve_hip_status_string": (C.c_char_p, [_i]),
     "nve_hip_version": (C.c_char_p, []),
@@ -58,6 +62,35 @@ class W4Mat(C.Structure):
     """nve_w4_mat (include/nve_kernels.h)."""
     _fields_ = [("nibbles", C.c_void_p), ("scales", C.c_void_p), ("awq", C.c_void_p), ("out", C.c_void_p),
                 ("n", C.c_int)]
+
+
+class DecodeConfig(C.Structure):
+    """nve_decode_config."""
+    _fields_ = [("hidden", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int), ("head_dim", C.c_int),
+                ("ffn", C.c_int), ("max_seq", C.c_int), ("vocab", C.c_int), ("eps", C.c_float)]
+
+
+class W4Weight(C.Structure):
+    """nve_w4_weight."""
+    _fields_ = [("nibbles", C.c_void_p), ("scales", C.c_void_p), ("n", C.c_int), ("k", C.c_int)]
+
+
+class LayerWeights(C.Structure):
+    """nve_layer_weights."""
+    _fields_ = [("input_norm", C.c_void_p), ("post_attn_norm", C.c_void_p)] + [
+        (nm, W4Weight) for nm in ("q", "k", "v", "o", "gate", "up", "down")]
+
+
+class DecodeIO(C.Structure):
+    """nve_decode_io."""
+    _fields_ = [("hidden", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("pos", C.c_void_p),
+                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("workspace", C.c_void_p)]
+
+
+class DecodeHead(C.Structure):
+    """nve_decode_head."""
+    _fields_ = [("hidden", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", W4Weight), ("embed", C.c_void_p),
+                ("logits", C.c_void_p), ("token_out", C.c_void_p), ("pos", C.c_void_p), ("workspace", C.c_void_p)]
 
 
 _lib: C.CDLL | None = None

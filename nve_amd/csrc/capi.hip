@@ -26,6 +26,9 @@ int launch_status() {
 static int from_hip(hipError_t e) { return set_status(e == hipSuccess ? NVE_OK : (int)e); }
 
 static bool dtype_ok(int dt) { return dt == NVE_DT_F16 || dt == NVE_DT_BF16 || dt == NVE_DT_F32; }
+// GEMV outputs additionally accept the fp32 accumulate mode.
+static bool out_ok(int dt) { return dtype_ok(dt) || dt == NVE_DT_F32_ACCUM; }
+static bool out_aligned(const void* p, int dt) { return aligned(p, dt >= NVE_DT_F32 ? 4 : 2); }
 
 // Common GEMV argument checks.
 static int check_gemv(const void* nib, const void* sc, const void* out, int N, int K) {
@@ -101,9 +104,8 @@ int nve_hip_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t*
   if (!xq || !xq_scales) return set_status(NVE_ERR_NULL);
   int st = check_gemv(nibbles, wt_scales, out, N, K);
   if (st != NVE_OK) return set_status(st);
-  if (!dtype_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
-  if (!aligned(xq, 16) || !aligned(xq_scales, 4) || (out_dtype == NVE_DT_F32 && !aligned(out, 4)))
-    return set_status(NVE_ERR_ALIGN);
+  if (!out_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (!aligned(xq, 16) || !aligned(xq_scales, 4) || !out_aligned(out, out_dtype)) return set_status(NVE_ERR_ALIGN);
   W4Segs s{};
   s.nseg = 1;
   s.nib[0] = nibbles;
@@ -117,13 +119,13 @@ int nve_hip_grouped_matvec_w4a8(const int8_t* xq, const float* xq_scales, const 
                                 int count, int out_dtype, int K, void* stream) {
   if (!xq || !xq_scales || !mats) return set_status(NVE_ERR_NULL);
   if (count < 1 || count > 3) return set_status(NVE_ERR_SHAPE);
-  if (!dtype_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (!out_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
   W4Segs s{};
   s.nseg = count;
   for (int i = 0; i < count; ++i) {
     int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K);
     if (st != NVE_OK) return set_status(st);
-    if (out_dtype == NVE_DT_F32 && !aligned(mats[i].out, 4)) return set_status(NVE_ERR_ALIGN);
+    if (!out_aligned(mats[i].out, out_dtype)) return set_status(NVE_ERR_ALIGN);
     s.nib[i] = mats[i].nibbles;
     s.sc[i] = mats[i].scales;
     s.out[i] = mats[i].out;
@@ -173,9 +175,9 @@ int nve_hip_matvec_w4a16(const void* x, int x_dtype, const uint8_t* nibbles, con
   if (!x) return set_status(NVE_ERR_NULL);
   int st = check_gemv(nibbles, scales, out, N, K);
   if (st != NVE_OK) return set_status(st);
-  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !dtype_ok(out_dtype))
+  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !out_ok(out_dtype))
     return set_status(NVE_ERR_DTYPE);
-  if (!aligned(x, 16) || (awq && !aligned(awq, 16)) || (out_dtype == NVE_DT_F32 && !aligned(out, 4)))
+  if (!aligned(x, 16) || (awq && !aligned(awq, 16)) || !out_aligned(out, out_dtype))
     return set_status(NVE_ERR_ALIGN);
   W4Segs s{};
   s.nseg = 1;
@@ -191,14 +193,14 @@ int nve_hip_grouped_matvec_w4a16(const void* x, int x_dtype, const nve_w4_mat* m
                                  int out_dtype, int K, void* stream) {
   if (!x || !mats) return set_status(NVE_ERR_NULL);
   if (count < 1 || count > 3) return set_status(NVE_ERR_SHAPE);
-  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !dtype_ok(out_dtype))
+  if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !out_ok(out_dtype))
     return set_status(NVE_ERR_DTYPE);
   W4Segs s{};
   s.nseg = count;
   for (int i = 0; i < count; ++i) {
     int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K);
     if (st != NVE_OK) return set_status(st);
-    if ((mats[i].awq && !aligned(mats[i].awq, 16)) || (out_dtype == NVE_DT_F32 && !aligned(mats[i].out, 4)))
+    if ((mats[i].awq && !aligned(mats[i].awq, 16)) || !out_aligned(mats[i].out, out_dtype))
       return set_status(NVE_ERR_ALIGN);
     s.nib[i] = mats[i].nibbles;
     s.sc[i] = mats[i].scales;
@@ -265,6 +267,57 @@ int nve_use_w4a8(double layer_importance) {
   double parsed;
   if (parse_f64_strict(getenv("NVE_W4A8_THRESHOLD"), &parsed)) threshold = parsed;
   return layer_importance < threshold ? 1 : 0;
+}
+
+// ---- decode step --------------------------------------------------------------------
+size_t nve_hip_decode_workspace_bytes(const nve_decode_config* cfg) {
+  return cfg ? decode_workspace_bytes(*cfg) : 0;
+}
+
+static int check_w4(const nve_w4_weight& w, int n, int k) {
+  if (!w.nibbles || !w.scales) return NVE_ERR_NULL;
+  if (w.n != n || w.k != k) return NVE_ERR_SHAPE;
+  if (!aligned(w.nibbles, 16) || !aligned(w.scales, 4)) return NVE_ERR_ALIGN;
+  return NVE_OK;
+}
+
+int nve_hip_layer_forward_decode(const nve_decode_config* cfg, const nve_layer_weights* w, const nve_decode_io* io,
+                                 int use_w4a8, void* stream) {
+  if (!cfg || !w || !io) return set_status(NVE_ERR_NULL);
+  int st = check_decode(*cfg);
+  if (st != NVE_OK) return set_status(st);
+  const int H = cfg->hidden, F = cfg->ffn, QD = cfg->num_heads * cfg->head_dim,
+            KD = cfg->num_kv_heads * cfg->head_dim;
+  const nve_w4_weight* mats[7] = {&w->q, &w->k, &w->v, &w->o, &w->gate, &w->up, &w->down};
+  const int ns[7] = {QD, KD, KD, H, F, F, H}, ks[7] = {H, H, H, QD, H, H, F};
+  for (int i = 0; i < 7; ++i)
+    if ((st = check_w4(*mats[i], ns[i], ks[i])) != NVE_OK) return set_status(st);
+  if (!w->input_norm || !w->post_attn_norm || !io->hidden || !io->k_cache || !io->v_cache || !io->pos ||
+      !io->rope_cos || !io->rope_sin || !io->workspace)
+    return set_status(NVE_ERR_NULL);
+  if (!aligned(io->workspace, 256) || !aligned(io->hidden, 16) || !aligned(io->k_cache, 16) ||
+      !aligned(io->v_cache, 16))
+    return set_status(NVE_ERR_ALIGN);
+  return set_status(layer_forward_decode(*cfg, *w, *io, use_w4a8 != 0, (hipStream_t)stream));
+}
+
+int nve_hip_decode_head(const nve_decode_config* cfg, const nve_decode_head* hd, int use_w4a8, void* stream) {
+  if (!cfg || !hd) return set_status(NVE_ERR_NULL);
+  int st = check_decode(*cfg);
+  if (st != NVE_OK) return set_status(st);
+  if ((st = check_w4(hd->lm_head, hd->lm_head.n, cfg->hidden)) != NVE_OK) return set_status(st);
+  if (hd->lm_head.n < 1 || (!hd->logits && hd->lm_head.n > cfg->vocab)) return set_status(NVE_ERR_SHAPE);
+  if (!hd->hidden || !hd->final_norm || !hd->embed || !hd->token_out || !hd->pos || !hd->workspace)
+    return set_status(NVE_ERR_NULL);
+  if (!aligned(hd->workspace, 256) || !aligned(hd->hidden, 16) || (hd->logits && !aligned(hd->logits, 4)))
+    return set_status(NVE_ERR_ALIGN);
+  return set_status(decode_head(*cfg, *hd, use_w4a8 != 0, (hipStream_t)stream));
+}
+
+int nve_hip_embed(const uint16_t* embed, const int* token, float* hidden, int hidden_size, void* stream) {
+  if (!embed || !token || !hidden) return set_status(NVE_ERR_NULL);
+  if (hidden_size < 1) return set_status(NVE_ERR_SHAPE);
+  return from_hip(launch_embed(embed, token, hidden, hidden_size, (hipStream_t)stream));
 }
 
 // ---- kernel selection ---------------------------------------------------------------

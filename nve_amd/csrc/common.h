@@ -114,6 +114,10 @@ template <>
 __device__ __forceinline__ void store_out<NVE_DT_F32>(void* p, size_t i, float v) {
   ((float*)p)[i] = v;
 }
+template <>
+__device__ __forceinline__ void store_out<NVE_DT_F32_ACCUM>(void* p, size_t i, float v) {
+  ((float*)p)[i] += v;  // one writer per row
+}
 
 // Barrier that waits only for this wave's LDS traffic (not for outstanding global
 // loads), so weight loads issued before it stay in flight across the barrier.
@@ -123,6 +127,36 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// int8 quantization of one value already multiplied by 1/scale: round half to even,
+// NaN -> 0, clamp to [-127, 127] (_nve_quantize_f16_q8, cuda/nve_kernels.cu:712-745).
+__device__ __forceinline__ int8_t q8_round_clamp(float v) {
+  float r = rintf(v);
+  if (r != r) r = 0.0f;  // NaN -> 0
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int8_t)(int)r;
+}
+
+// Group-32 int8 quantization of 4 consecutive values per lane, 8 consecutive lanes per
+// group (all 8 lanes of a group must be active): scale = absmax / 127 (1 for an
+// all-zero group), codes = q8_round_clamp(v / scale); element i0 is the lane's first.
+__device__ __forceinline__ void q8_group8_store(const float v[4], bool ok, int8_t* __restrict__ xq,
+                                                float* __restrict__ xs, size_t i0) {
+  float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  m = quad_max_f(m);
+  m = fmaxf(m, dpp_mov<0x141>(m));  // row_half_mirror: the other quad of the 8 lanes
+  const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+  const float inv = 1.0f / scale;
+  if (ok) {
+    char4 q;
+    q.x = q8_round_clamp(v[0] * inv);
+    q.y = q8_round_clamp(v[1] * inv);
+    q.z = q8_round_clamp(v[2] * inv);
+    q.w = q8_round_clamp(v[3] * inv);
+    *(char4*)(xq + i0) = q;
+    if ((i0 & 31) == 0) xs[i0 >> 5] = scale;
+  }
 }
 
 }  // namespace nve

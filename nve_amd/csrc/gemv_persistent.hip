@@ -80,6 +80,7 @@ static hipError_t launch_p_any(const typename P::Args& a, const W4Segs& segs, in
   switch (out_dt) {
     case NVE_DT_F16: return launch_p_dt<P, NVE_DT_F16>(a, segs, K, stream);
     case NVE_DT_BF16: return launch_p_dt<P, NVE_DT_BF16>(a, segs, K, stream);
+    case NVE_DT_F32_ACCUM: return launch_p_dt<P, NVE_DT_F32_ACCUM>(a, segs, K, stream);
     default: return launch_p_dt<P, NVE_DT_F32>(a, segs, K, stream);
   }
 }

@@ -213,6 +213,7 @@ hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt,
   switch (out_dt) {
     case NVE_DT_F16: return launch_w4a16_o<NVE_DT_F16>(x, x_dt, segs, K, stream);
     case NVE_DT_BF16: return launch_w4a16_o<NVE_DT_BF16>(x, x_dt, segs, K, stream);
+    case NVE_DT_F32_ACCUM: return launch_w4a16_o<NVE_DT_F32_ACCUM>(x, x_dt, segs, K, stream);
     default: return launch_w4a16_o<NVE_DT_F32>(x, x_dt, segs, K, stream);
   }
 }

@@ -182,6 +182,7 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
   switch (out_dt) {
     case NVE_DT_F16: return launch_w4a8_dt<NVE_DT_F16>(xq, xs, segs, K, stream);
     case NVE_DT_BF16: return launch_w4a8_dt<NVE_DT_BF16>(xq, xs, segs, K, stream);
+    case NVE_DT_F32_ACCUM: return launch_w4a8_dt<NVE_DT_F32_ACCUM>(xq, xs, segs, K, stream);
     default: return launch_w4a8_dt<NVE_DT_F32>(xq, xs, segs, K, stream);
   }
 }

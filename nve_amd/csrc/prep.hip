@@ -10,13 +10,6 @@ namespace nve {
 // amax/127 : 1; q = clamp(rne(x * (1/scale)), -127, 127).  Division and reciprocal
 // are IEEE binary32 (correctly rounded); rne is v_rndne_f32.
 // Thread layout: 8 lanes per group, 4 activations per lane.
-__device__ __forceinline__ int8_t q8_round_clamp(float v) {
-  float r = rintf(v);
-  if (r != r) r = 0.0f;  // NaN -> 0
-  r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return (int8_t)(int)r;
-}
-
 template <int XDT>
 __device__ __forceinline__ void load4(const void* x, size_t i4, float v[4]) {
   if (XDT == NVE_DT_F32) {

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/nve_kernels.h"
+
 // Up to three weight matrices that share one activation vector and K (Q/K/V).
 // Workgroups [wg_begin[s], wg_begin[s+1]) compute matrix s.
 struct W4Segs {
@@ -163,6 +165,12 @@ hipError_t launch_w4a8_persistent(const int8_t* xq, const float* xs, W4Segs segs
                                   hipStream_t stream);
 hipError_t launch_w4a16_persistent(const void* x, int x_dt, W4Segs segs, int out_dt, int K,
                                    hipStream_t stream);
+size_t decode_workspace_bytes(const nve_decode_config& c);
+int check_decode(const nve_decode_config& c);
+int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
+                         bool w4a8, hipStream_t s);
+int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8, hipStream_t s);
+hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);
 hipError_t launch_w4a8_block_acc(const int8_t* xq, const uint8_t* nib, int32_t* acc, int N, int K,

@@ -87,6 +87,43 @@ def test_batched_and_prep_argument_errors(L):
                                       P16, P16, P16, 0, 64, None) == -2
 
 
+def test_decode_argument_errors(L):
+    from nve_amd._lib import DecodeConfig, DecodeHead, DecodeIO, LayerWeights, W4Weight
+    H, F, D, hq, hkv = 256, 512, 64, 4, 2
+
+    def w(n, k):
+        return W4Weight(P16, P16, n, k)
+
+    def weights(**over):
+        d = dict(q=w(hq * D, H), k=w(hkv * D, H), v=w(hkv * D, H), o=w(H, hq * D), gate=w(F, H), up=w(F, H),
+                 down=w(H, F))
+        d.update(over)
+        return LayerWeights(P16, P16, d["q"], d["k"], d["v"], d["o"], d["gate"], d["up"], d["down"])
+
+    io = DecodeIO(P16, P16, P16, P16, P16, P16, P16)
+    f = L.nve_hip_layer_forward_decode
+
+    def call(cfg, wts=None, iox=io):
+        return f(C.byref(cfg), C.byref(wts or weights()), C.byref(iox), 1, None)
+
+    assert call(DecodeConfig(H, hq, hkv, 96, F, 64, 512, 1e-5)) == -2        # head_dim 96
+    assert call(DecodeConfig(H, 12, 1, D, F, 64, 512, 1e-5)) == -2           # 12 q heads per kv head
+    assert call(DecodeConfig(H + 16, hq, hkv, D, F, 64, 512, 1e-5)) == -2    # H % 32
+    assert call(DecodeConfig(H, hq, hkv, D, F, 16385, 512, 1e-5)) == -5      # cache past the combine's limit
+    assert call(DecodeConfig(H, hq, hkv, 256, F, 8193, 512, 1e-5),
+                weights(q=w(hq * 256, H), k=w(hkv * 256, H), v=w(hkv * 256, H), o=w(H, hq * 256))) == -5
+    cfg = DecodeConfig(H, hq, hkv, D, F, 64, 512, 1e-5)
+    assert call(cfg, weights(gate=w(F, H + 32))) == -2                       # weight shape mismatch
+    assert call(cfg, weights(down=W4Weight(None, P16, H, F))) == -1
+    assert call(cfg, weights(o=W4Weight(P16 + 4, P16, H, hq * D))) == -3
+    assert call(cfg, iox=DecodeIO(P16, P16, P16, None, P16, P16, P16)) == -1  # pos
+    assert call(cfg, iox=DecodeIO(P16, P16, P16, P16, P16, P16, P16 + 16)) == -3  # workspace alignment
+    bad = DecodeHead(P16, P16, w(512, H + 32), P16, P16, P16, P16, P16)
+    assert L.nve_hip_decode_head(C.byref(cfg), C.byref(bad), 1, None) == -2
+    assert L.nve_hip_embed(None, P16, P16, H, None) == -1
+    assert L.nve_hip_decode_workspace_bytes(C.byref(cfg)) % 256 == 0
+
+
 def test_dispatch_env_rules(L, orc, monkeypatch):
     """nve_use_w4a8 (src/gpu_layer.rs:1013-1025) against the oracle's truth table."""
     monkeypatch.delenv("NVE_NO_W4A8", raising=False)

@@ -1,0 +1,147 @@
+"""GPU parity of the decode step (nve_hip_layer_forward_decode + nve_hip_decode_head)
+against the CPU restatement oracle/decode_ref.emulate_step, on small synthetic models.
+
+Every layer and the head are teacher-forced: the oracle's layer starts from the GPU's
+hidden state before that layer, so each is checked on its own.  Bars:
+  * a layer's contribution (h_out - h_in) and the logits: ||gpu - oracle|| / ||oracle||
+    <= 2e-3 (W4A8 activations are re-quantized at every projection input, so a
+    last-ulp difference upstream can move an int8 code);
+  * token: the GPU's token is the first maximum of the GPU's own logits (exact), and
+    equals the oracle's whenever the oracle's top-2 gap exceeds the logit error;
+  * KV cache: the slot written at pos equals the oracle's bf16 row to 1 bf16 ulp
+    (plus 2e-3 of the row's rms for entries near zero);
+  * HIP graph replay reproduces the eager sequence bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import rel_err_norm
+
+pytestmark = pytest.mark.gpu
+
+TOL_LAYER = 2e-3
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def _model(torch, heads, kv, d, *, layers=3, hidden=256, ffn=512, vocab=512, max_seq=160, prefill=60,
+           importance=(0.0, 1.0, 0.0), lm_head_w4a8=True, seed=11):
+    from nve_amd.decode import DecodeModel, ModelShape
+    shape = ModelShape(hidden=hidden, layers=layers, heads=heads, kv_heads=kv, head_dim=d, ffn=ffn, vocab=vocab,
+                       rope_theta=10000.0)
+    imp = np.array(importance[:layers], np.float64)
+    return DecodeModel(shape, max_seq=max_seq, prefill=prefill, importance=imp, lm_head_w4a8=lm_head_w4a8,
+                       seed=seed)
+
+
+def _run_teacher_forced(torch, m, steps, token0=5):
+    """Layer by layer: the oracle's layer i starts from the GPU's hidden state before
+    layer i, so every layer and the head are checked on their own."""
+    from oracle import decode_ref as dr
+    hm = dr.HostModel(m)
+    m.start(token0)
+    pos = m.prefill
+    errs = []
+    for i in range(steps):
+        print(f"decode step {i} pos {pos}", flush=True)
+        m._advance(1)
+        for li in range(m.shape.layers):
+            torch.cuda.synchronize()
+            h_in = m.hidden.cpu().numpy().copy()
+            m.layer(li)
+            torch.cuda.synchronize()
+            h_gpu = m.hidden.cpu().numpy()
+            h_ora = dr.emulate_layer(hm, li, h_in, pos)
+            err = rel_err_norm(h_gpu - h_in, h_ora - h_in)  # the layer's own contribution
+            errs.append(("layer", li, m.use_w4a8[li], err))
+            assert err <= TOL_LAYER, (i, li, err)
+            for name in ("k_cache", "v_cache"):
+                g_row = dr.bf16_to_f32(m.layers[li][name][:, pos].view(torch.int16).cpu().numpy().view(np.uint16))
+                o_row = hm.layers[li][name][:, pos]
+                # one bf16 ulp, plus the projection's own error on near-zero entries
+                tol = np.abs(o_row) * 2.0 ** -7 + TOL_LAYER * np.sqrt(np.mean(o_row ** 2))
+                assert np.all(np.abs(g_row - o_row) <= tol), (i, li, name)
+        h_in = m.hidden.cpu().numpy().copy()
+        m.head()
+        torch.cuda.synchronize()
+        g_logits = m.logits.cpu().numpy()
+        g_tok = int(m.token.item())
+        o_logits, o_tok = dr.emulate_head(hm, h_in)
+        err = rel_err_norm(g_logits, o_logits)
+        errs.append(("head", -1, m.lm_head_w4a8, err))
+        assert err <= TOL_LAYER, (i, err)
+        assert g_tok == int(np.argmax(g_logits))
+        top = np.sort(o_logits)[-2:]
+        if top[1] - top[0] > 4 * TOL_LAYER * np.linalg.norm(o_logits) / np.sqrt(o_logits.size):
+            assert g_tok == o_tok, (i, g_tok, o_tok)
+        # the head embedded the GPU's token and advanced the position
+        assert np.array_equal(m.hidden.cpu().numpy(), hm.embed[g_tok])
+        assert int(m.pos.item()) == pos + 1
+        pos += 1
+    print("max errors:", {k: max(e[3] for e in errs if (e[0], e[2]) == k)
+                          for k in {(e[0], e[2]) for e in errs}}, flush=True)
+    return m
+
+
+@pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256)])
+def test_decode_step_mixed_precision(torch_dev, heads, kv, d):
+    m = _model(torch_dev, heads, kv, d)
+    _run_teacher_forced(torch_dev, m, steps=6)  # pos 60..65 crosses the 64-key chunk edge
+
+
+@pytest.mark.parametrize("importance,lm8", [((0.0, 0.0), True), ((1.0, 1.0), False)])
+def test_decode_step_single_precision(torch_dev, importance, lm8):
+    m = _model(torch_dev, 4, 1, 128, layers=2, importance=importance, lm_head_w4a8=lm8, prefill=1, max_seq=64)
+    _run_teacher_forced(torch_dev, m, steps=3)
+
+
+def test_decode_empty_prefill_and_last_slot(torch_dev):
+    # prefill 0: the first step attends to its own key only; the last steps fill the cache
+    m = _model(torch_dev, 4, 2, 64, layers=2, prefill=0, max_seq=4)
+    _run_teacher_forced(torch_dev, m, steps=4)
+    with pytest.raises(ValueError):
+        m.step()
+
+
+def test_decode_graph_replay_matches_eager(torch_dev):
+    torch = torch_dev
+    m = _model(torch, 4, 2, 64, max_seq=96, prefill=40)
+    n = 8
+    m.start(9)
+    toks, logits = [], []
+    for _ in range(n):
+        m.step()
+        toks.append(int(m.token.item()))
+        logits.append(m.logits.cpu().numpy().copy())
+    m.start(9)
+    m.capture()
+    for r in range(n):
+        m.generate(1)
+        torch.cuda.synchronize()
+        assert int(m.token.item()) == toks[r], r
+        assert np.array_equal(m.logits.cpu().numpy(), logits[r]), r
+    assert int(m.pos.item()) == 40 + n
+
+
+def test_decode_3b_shape_smoke(torch_dev):
+    """The Llama-3.2-3B shapes (head_dim 128, GQA 3, ffn 8192, vocab 128256) on 2 layers:
+    one teacher-forced step against the oracle over the full logits."""
+    from nve_amd.decode import ModelShape, DecodeModel
+    s = ModelShape(layers=2)
+    m = DecodeModel(s, max_seq=130, prefill=128, importance=np.array([0.0, 1.0]))
+    _run_teacher_forced(torch_dev, m, steps=1)
+
+
+def test_decode_split_attention_long_cache(torch_dev):
+    """max_seq above the single-pass limit takes the split-sequence kernel with the
+    cross-workgroup combine; pos 8190..8192 crosses a 64-key chunk edge."""
+    m = _model(torch_dev, 4, 2, 64, layers=2, importance=(0.0, 1.0), max_seq=8256, prefill=8190)
+    _run_teacher_forced(torch_dev, m, steps=3)
