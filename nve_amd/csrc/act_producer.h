@@ -1,0 +1,129 @@
+// act_producer.h -- activation producers fused into the GEMV staging.
+//
+// A decode layer feeds its GEMVs with vectors that a small elementwise kernel would
+// otherwise produce just before (RMSNorm of the residual, the int8 quantization of
+// silu(gate) * up).  Every
+// GEMV workgroup stages the whole activation vector in LDS anyway, so it can compute
+// that vector itself from the producer's inputs: the loads are issued with the
+// staging loads (ahead of the weight loads), the arithmetic runs while the weight
+// loads are in flight, and one kernel launch per producer disappears.  The output of
+// a producer is the same f32 value the standalone kernel computes; the GEMV then
+// quantizes it to int8 with group-32 scales (W4A8) or rounds it to bf16 (W4A16)
+// exactly as the standalone path does.
+//
+//   SRC_NORM: x_k = h_k * w_k / sqrt(mean(h^2) + eps), sum of squares and scaling in
+//             f64 (src/ops.rs:12-30); a = h (f32 [K]), b = w (bf16 [K]).
+//   SRC_F32:  x_k = a_k (an f32 vector, e.g. silu(gate) * up written by the SwiGLU
+//             epilogue of the gate/up GEMV); b unused.
+#pragma once
+
+#include "common.h"
+
+namespace nve {
+
+enum { SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2 };
+
+struct ProdArgs {
+  const float* a;
+  const void* b;
+  float eps;
+};
+
+// E activations (8 or 16) of one staging chunk.
+template <int SRC, int E>
+struct ProdChunk {
+  float4 a[E / 4];
+  uint4 b[SRC == SRC_NORM ? E / 8 : 1];
+};
+
+template <int SRC, int E>
+__device__ __forceinline__ void prod_issue(ProdChunk<SRC, E>& c, const ProdArgs& p, int chunk, int nchunk) {
+  const int i = min(chunk, nchunk - 1);
+#pragma unroll
+  for (int t = 0; t < E / 4; ++t) c.a[t] = ((const float4*)p.a)[i * (E / 4) + t];
+  if constexpr (SRC == SRC_NORM) {
+#pragma unroll
+    for (int t = 0; t < E / 8; ++t) c.b[t] = ((const uint4*)p.b)[i * (E / 8) + t];
+  }
+}
+
+// Sum of squares of the valid chunks of this thread (SRC_NORM), in f64.
+template <int SRC, int E, int SPT>
+__device__ __forceinline__ double prod_sumsq(const ProdChunk<SRC, E> (&c)[SPT], int nchunk) {
+  double ss = 0.0;
+#pragma unroll
+  for (int s = 0; s < SPT; ++s) {
+    const bool ok = (int)threadIdx.x + 256 * s < nchunk;
+#pragma unroll
+    for (int t = 0; t < E / 4; ++t) {
+      const float4 v = c[s].a[t];
+      const double q = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+      ss += ok ? q : 0.0;
+    }
+  }
+  return ss;
+}
+
+// 1 / sqrt(mean(h^2) + eps) over the K elements, reduced over the 256 threads of the
+// workgroup (wave butterflies, then 4 partials through LDS).  Every workgroup sums in
+// the same order, so all of them produce the same value.
+__device__ __forceinline__ double prod_norm_inv(double ss, int K, float eps, double* s_red) {
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+  lds_barrier();
+  const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  return 1.0 / sqrt(tot / (double)K + (double)eps);
+}
+
+template <int SRC, int E>
+__device__ __forceinline__ void prod_values(const ProdChunk<SRC, E>& c, double inv, float (&v)[E]) {
+#pragma unroll
+  for (int t = 0; t < E / 4; ++t) {
+    const float a4[4] = {c.a[t].x, c.a[t].y, c.a[t].z, c.a[t].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 4 * t + e;
+      if (SRC == SRC_NORM) {
+        const uint4 wb = c.b[k / 8];
+        const uint32_t wd[4] = {wb.x, wb.y, wb.z, wb.w};
+        const uint32_t pair = wd[(k % 8) / 2];
+        const float w = bf16_bits_to_f32((k & 1) ? (pair >> 16) : (pair & 0xffffu));
+        v[k] = (float)((double)a4[e] * inv * (double)w);
+      } else {
+        v[k] = a4[e];
+      }
+    }
+  }
+}
+
+// W4A8: 16 values of a half block -> 16 int8 codes; the block's scale comes from the
+// absmax over the two lanes (2k, 2k+1) holding the block (nve_quantize_f16_q8 rule).
+__device__ __forceinline__ int4 prod_quant16(const float (&v)[16], float& scale_out) {
+  float m = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(v[e]));
+  m = fmaxf(m, dpp_mov<0xB1>(m));  // quad_perm [1,0,3,2]: the pair partner
+  const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+  const float inv = 1.0f / scale;
+  uint32_t d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w |= (uint32_t)(uint8_t)q8_round_clamp(v[4 * t + e] * inv) << (8 * e);
+    d[t] = w;
+  }
+  scale_out = scale;
+  return make_int4((int)d[0], (int)d[1], (int)d[2], (int)d[3]);
+}
+
+// W4A16: 8 values -> 8 bf16 (round to nearest even), as the standalone producers store.
+__device__ __forceinline__ uint4 prod_bf16x8(const float (&v)[8]) {
+  uint32_t d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    d[t] = (uint32_t)f32_to_bf16_bits(v[2 * t]) | ((uint32_t)f32_to_bf16_bits(v[2 * t + 1]) << 16);
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+}  // namespace nve

@@ -11,17 +11,13 @@
 // pairs 264-276, silu 62-64, softmax 152-163, argmax 485-495 first maximum) and
 // src/attention.rs:149-228 (GQA, scale 1/sqrt(head_dim)).
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
+#include "act_producer.h"
 #include "w4_launch.h"
 
 namespace nve {
-
-// Keys per attention work item: 64 (32 for head_dim 256, to keep the K/V tiles of a
-// workgroup within 64 KB of LDS).
-__host__ __device__ constexpr int attn_chunk(int D) { return D == 256 ? 32 : 64; }
-// Chunks per kv head the combine holds in LDS (max_seq <= 256 * attn_chunk(D)).
-constexpr int kAttnMaxChunks = 256;
 
 // Loads that must see other workgroups' stores from the same launch (after their
 // release fence): device-scope atomic loads bypass the CU's vector L1.
@@ -79,357 +75,125 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 }
 
 // ---- attention ------------------------------------------------------------------
-// One launch per layer: RoPE on q and on the new key, KV-cache append, split-sequence
-// softmax(q k^T / sqrt(D)) v over the cached keys, the cross-chunk combine, and the
-// conversion of the attention output to the o_proj input (OUT 1: bf16, OUT 2: int8 +
-// group-32 scales).
+// One launch per layer: RoPE on q and on the new key, KV-cache append,
+// softmax(q k^T / sqrt(D)) v over the cache, and the conversion of the output to the
+// o_proj input (OUT 1: bf16, OUT 2: int8 + group-32 scales).
 //
-// grid (num_kv_heads, ceil(max_seq / KC)), 256 threads; chunks at or past pos + 1
-// exit at once.  A workgroup stages its KC keys and values (bf16 rows of D) in LDS
-// with every global load issued up front, computes the G = num_heads / num_kv_heads
-// query heads of its kv head against them (4 or 8 threads per key for the scores,
-// 2-dimension columns x key groups for the value sum), and writes a partial (running
-// max m, sum l, unnormalised acc[D]) per query head.  The last workgroup of a kv
-// head to finish (a device-scope counter, reset by that workgroup, so replays of a
-// captured graph need no memset) combines the partials:
-//   out[d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c.
-// The chunk holding pos rotates the new key, rounds key and value to bf16 like every
-// cached entry, writes them to the cache and uses them from LDS.
-template <int D, int OUT>
-__global__ __launch_bounds__(256) void attn_decode_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
-    int max_seq, float scale, float* __restrict__ part, int* __restrict__ counters,
-    uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q, float* __restrict__ out_s) {
-  constexpr int NT = 256;
-  constexpr int KC = attn_chunk(D);
-  constexpr int HALF = D / 2;
-  constexpr int G_MAX = 8;
-  constexpr int ROW = D + 8;                 // padded LDS row, bf16 elements
-  constexpr int U4_ROW = D / 8;              // 16-byte pieces per row
-  constexpr int U4_T = KC * U4_ROW / NT;     // pieces per thread (2 or 4)
-  constexpr int TPK = NT / KC;               // score threads per key (4 or 8)
-  constexpr int DPT = D / TPK;               // dims per score thread (16 or 32)
-  constexpr int DP = D / 2;                  // value columns (dimension pairs)
-  constexpr int KG = NT / DP;                // key groups of the value sum
-  constexpr int KPG = KC / KG;               // keys per key group
-  static_assert(U4_T * NT == KC * U4_ROW && DPT % 8 == 0 && KG * DP == NT, "attention tiling");
-  static_assert(2 * G_MAX * kAttnMaxChunks <= KG * G_MAX * D, "combine weights fit in s_red");
+// One workgroup of 16 waves per query head; no cross-workgroup communication.  Keys
+// are spread over the waves in tiles: a key's row of D bf16 (D/8 16-byte pieces)
+// sits in LPK = D/8 consecutive lanes, one piece per lane, so the q.k dot product is
+// a butterfly over those lanes and the value sum accumulates each lane's 8 columns.
+// Every wave keeps its own online softmax (running max m, sum l, accumulator
+// rescaled by e^(m_old - m_new)) over its keys, with the next tile's K/V loads in
+// flight while the current tile is computed; the 16 wave states are merged once in
+// LDS at the end:  out = sum_w e^(m_w - M) acc_w / sum_w e^(m_w - M) l_w.
+// The new token's key is rotated and rounded to bf16 like every cached entry; the
+// workgroup of the kv head's first query head writes it and the value to the cache,
+// the others use their own identical copy for that row.
+template <int D>
+struct AttnTile {
+  static constexpr int NW = 16;         // waves per workgroup
+  static constexpr int P = 2;           // key slots per lane per tile
+  static constexpr int LPK = D / 8;     // lanes per key
+  static constexpr int KPW = 64 / LPK;  // keys per wave per slot
+  static constexpr int KT = NW * KPW * P;
+  uint4 k[P], v[P];
+};
 
-  __shared__ __align__(16) uint16_t s_k[KC * ROW];
-  __shared__ __align__(16) uint16_t s_v[KC * ROW];
-  __shared__ float s_q[G_MAX * D];
-  __shared__ __align__(16) uint16_t s_knew[D];
-  __shared__ __align__(16) uint16_t s_vnew[D];
-  __shared__ float s_p[G_MAX][KC];
-  __shared__ float s_ml[G_MAX][2];
-  __shared__ int s_last;
-  __shared__ float s_red[KG * G_MAX * D];  // value-sum partials of the key groups (16 KB)
-
-  const int kvh = blockIdx.x;
-  const int c = blockIdx.y;
-  const int tid = threadIdx.x;
-  // a position past the cache is clamped to its last slot (the host bounds the step
-  // count; the clamp only keeps every access inside the cache and the RoPE tables)
-  const int pos = min(max(*d_pos, 0), max_seq - 1);
-  const int len = pos + 1;
-  const int t0 = c * KC;
-  if (t0 >= len) return;
-  const int G = num_heads / num_kv_heads;
-  const int nt = min(KC, len - t0);
-  const int nchunk = (max_seq + KC - 1) / KC;
-  const int used = (len + KC - 1) / KC;
-  const size_t cache_base = (size_t)kvh * max_seq * D;
-  const bool owner = pos < t0 + KC;  // this chunk holds the new token
-
-  // 1. every K/V load of the tile in flight (rows past nt re-read row t0)
-  uint4 rk[U4_T], rv[U4_T];
+template <int D>
+__device__ __forceinline__ void attn_issue(AttnTile<D>& b, const uint16_t* __restrict__ kc,
+                                           const uint16_t* __restrict__ vc, size_t cache_base, int t, int len,
+                                           int wave, int krow, int col) {
+  using T = AttnTile<D>;
 #pragma unroll
-  for (int i = 0; i < U4_T; ++i) {
-    const int piece = tid + i * NT;
-    const int row = piece / U4_ROW, col = piece % U4_ROW;
-    const size_t off = cache_base + (size_t)(t0 + (row < nt ? row : 0)) * D + col * 8;
-    rk[i] = *(const uint4*)(kc + off);
-    rv[i] = *(const uint4*)(vc + off);
-  }
-  // 2. rotated q of the G heads; the new key/value (owner)
-  const float* cs = rope_cos + (size_t)pos * HALF;
-  const float* sn = rope_sin + (size_t)pos * HALF;
-  for (int idx = tid; idx < G * HALF; idx += NT) {
-    const int g = idx / HALF, i = idx % HALF;
-    const float* qh = q + (size_t)(kvh * G + g) * D;
-    const float q0 = qh[i], q1 = qh[i + HALF];
-    s_q[g * D + i] = q0 * cs[i] - q1 * sn[i];
-    s_q[g * D + i + HALF] = q0 * sn[i] + q1 * cs[i];
-  }
-  if (owner) {
-    const float* kh = k + (size_t)kvh * D;
-    const float* vh = v + (size_t)kvh * D;
-    uint16_t* kdst = kc + cache_base + (size_t)pos * D;
-    uint16_t* vdst = vc + cache_base + (size_t)pos * D;
-    for (int i = tid; i < HALF; i += NT) {
-      const float k0 = kh[i], k1 = kh[i + HALF];
-      const uint16_t r0 = f32_to_bf16_bits(k0 * cs[i] - k1 * sn[i]);
-      const uint16_t r1 = f32_to_bf16_bits(k0 * sn[i] + k1 * cs[i]);
-      s_knew[i] = r0;
-      s_knew[i + HALF] = r1;
-      kdst[i] = r0;
-      kdst[i + HALF] = r1;
-    }
-    for (int i = tid; i < D; i += NT) {
-      const uint16_t r = f32_to_bf16_bits(vh[i]);
-      s_vnew[i] = r;
-      vdst[i] = r;
-    }
-  }
-  lds_barrier();
-  // 3. tile to LDS (the row of pos from the freshly rounded key/value)
-  const int prow = owner ? pos - t0 : -1;
-#pragma unroll
-  for (int i = 0; i < U4_T; ++i) {
-    const int piece = tid + i * NT;
-    const int row = piece / U4_ROW, col = piece % U4_ROW;
-    uint4 a = rk[i], b = rv[i];
-    if (row == prow) {
-      a = *(const uint4*)(s_knew + col * 8);
-      b = *(const uint4*)(s_vnew + col * 8);
-    }
-    *(uint4*)(s_k + row * ROW + col * 8) = a;
-    *(uint4*)(s_v + row * ROW + col * 8) = b;
-  }
-  lds_barrier();
-  // 4. scores: TPK threads per key, DPT dims each
-  {
-    const int j = tid / TPK, r = tid % TPK;
-    float sc[G_MAX];
-#pragma unroll
-    for (int g = 0; g < G_MAX; ++g) sc[g] = 0.0f;
-#pragma unroll
-    for (int d0 = 0; d0 < DPT; d0 += 8) {
-      const uint4 raw = *(const uint4*)(s_k + j * ROW + r * DPT + d0);
-      const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int u2 = 0; u2 < 4; ++u2) {
-        const float ka = bf16_bits_to_f32(wv[u2] & 0xffffu), kb = bf16_bits_to_f32(wv[u2] >> 16);
-        const int dd = r * DPT + d0 + 2 * u2;
-#pragma unroll
-        for (int g = 0; g < G_MAX; ++g)
-          if (g < G) sc[g] = fmaf(s_q[g * D + dd + 1], kb, fmaf(s_q[g * D + dd], ka, sc[g]));
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G_MAX; ++g) {
-      if (g >= G) break;
-      float s = sc[g];
-#pragma unroll
-      for (int off = 1; off < TPK; off <<= 1) s += __shfl_xor(s, off, 64);
-      if (r == 0) s_p[g][j] = j < nt ? s * scale : -INFINITY;
-    }
-  }
-  lds_barrier();
-  // 5. chunk softmax statistics (wave 0; lane = key)
-  if (tid < 64) {
-    for (int g = 0; g < G; ++g) {
-      const float s = tid < KC ? s_p[g][tid] : -INFINITY;
-      float m = s;
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-      const float p = s == -INFINITY ? 0.0f : expf(s - m);
-      float l = p;
-      for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
-      if (tid < KC) s_p[g][tid] = p;
-      if (tid == 0) {
-        s_ml[g][0] = m;
-        s_ml[g][1] = l;
-      }
-    }
-  }
-  lds_barrier();
-  // 6. value sum: column pair dp, key group kg
-  {
-    const int dp = tid % DP, kg = tid / DP;
-    float a0[G_MAX], a1[G_MAX];
-#pragma unroll
-    for (int g = 0; g < G_MAX; ++g) a0[g] = a1[g] = 0.0f;
-#pragma unroll 4
-    for (int jj = 0; jj < KPG; ++jj) {
-      const int j = kg * KPG + jj;
-      const uint32_t w2 = *(const uint32_t*)(s_v + j * ROW + 2 * dp);
-      const float va = bf16_bits_to_f32(w2 & 0xffffu), vb = bf16_bits_to_f32(w2 >> 16);
-#pragma unroll
-      for (int g = 0; g < G_MAX; ++g)
-        if (g < G) {
-          const float p = s_p[g][j];
-          a0[g] = fmaf(p, va, a0[g]);
-          a1[g] = fmaf(p, vb, a1[g]);
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G_MAX; ++g)
-      if (g < G) {
-        s_red[(kg * G_MAX + g) * D + 2 * dp] = a0[g];
-        s_red[(kg * G_MAX + g) * D + 2 * dp + 1] = a1[g];
-      }
-  }
-  lds_barrier();
-  // 7. partials to global, then the per-kv-head arrival counter
-  for (int idx = tid; idx < G * D; idx += NT) {
-    const int g = idx / D, d = idx % D;
-    float a = 0.0f;
-#pragma unroll
-    for (int kg = 0; kg < KG; ++kg) a += s_red[(kg * G_MAX + g) * D + d];
-    float* pp = part + ((size_t)(kvh * G + g) * nchunk + c) * (D + 2);
-    pp[2 + d] = a;
-    if (d == 0) {
-      pp[0] = s_ml[g][0];
-      pp[1] = s_ml[g][1];
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&counters[kvh], 1) == used - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // 8. last workgroup of this kv head: combine its G heads and emit the o_proj input.
-  // Chunk statistics first (one thread per (head, chunk), all loads in flight), then
-  // per-chunk weights f_c = e^(m_c - M) / sum_c' e^(m_c' - M) l_c' in LDS, then the
-  // weighted sum of the partial accumulators (loads unrolled by 4).
-  __threadfence();
-  if (tid == 0) atomicExch(&counters[kvh], 0);
-  float* s_f = s_red;  // [G][used] chunk weights, then [G][used] f*l (the value-sum partials are consumed)
-  const int ncomb = used;  // <= kAttnMaxChunks (host check): 2 * G * ncomb fits in s_red
-  for (int idx = tid; idx < G * ncomb; idx += NT) {
-    const int g = idx / ncomb, cc = idx % ncomb;
-    const float* p = part + ((size_t)(kvh * G + g) * nchunk + cc) * (D + 2);
-    s_f[g * ncomb + cc] = ld_agent(p);
-  }
-  __syncthreads();
-  if (tid < G) {
-    const int g = tid;
-    float M = -INFINITY;
-    for (int cc = 0; cc < ncomb; ++cc) M = fmaxf(M, s_f[g * ncomb + cc]);
-    s_ml[g][0] = M;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < G * ncomb; idx += NT) {
-    const int g = idx / ncomb, cc = idx % ncomb;
-    const float* p = part + ((size_t)(kvh * G + g) * nchunk + cc) * (D + 2);
-    const float f = expf(s_f[g * ncomb + cc] - s_ml[g][0]);
-    s_f[g * ncomb + cc] = f;
-    s_red[G * ncomb + g * ncomb + cc] = f * ld_agent(p + 1);
-  }
-  __syncthreads();
-  if (tid < G) {
-    const int g = tid;
-    float L = 0.0f;
-    for (int cc = 0; cc < ncomb; ++cc) L += s_red[G * ncomb + g * ncomb + cc];
-    s_ml[g][1] = 1.0f / L;
-  }
-  __syncthreads();
-  for (int e0 = 4 * tid; e0 < G * D; e0 += 4 * NT) {  // G*D % 32 == 0: 8-lane groups stay whole
-    const int g = e0 / D, d = e0 % D;
-    const float* pb = part + (size_t)(kvh * G + g) * nchunk * (D + 2) + 2 + d;
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    int cc = 0;
-    for (; cc + 4 <= ncomb; cc += 4) {
-      float4 x[4];
-#pragma unroll
-      for (int u2 = 0; u2 < 4; ++u2) {
-        const float* p = pb + (size_t)(cc + u2) * (D + 2);
-        x[u2] = make_float4(ld_agent(p), ld_agent(p + 1), ld_agent(p + 2), ld_agent(p + 3));
-      }
-#pragma unroll
-      for (int u2 = 0; u2 < 4; ++u2) {
-        const float f = s_f[g * ncomb + cc + u2];
-        o[0] = fmaf(f, x[u2].x, o[0]);
-        o[1] = fmaf(f, x[u2].y, o[1]);
-        o[2] = fmaf(f, x[u2].z, o[2]);
-        o[3] = fmaf(f, x[u2].w, o[3]);
-      }
-    }
-    for (; cc < ncomb; ++cc) {
-      const float* p = pb + (size_t)cc * (D + 2);
-      const float f = s_f[g * ncomb + cc];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) o[t] = fmaf(f, ld_agent(p + t), o[t]);
-    }
-    const float invL = s_ml[g][1];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) o[t] *= invL;
-    const size_t i0 = (size_t)(kvh * G + g) * D + d;
-    if (OUT == 1) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) out_bf16[i0 + t] = f32_to_bf16_bits(o[t]);
-    } else {
-      q8_group8_store(o, true, out_q, out_s, i0);
-    }
+  for (int i = 0; i < T::P; ++i) {
+    const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
+    const size_t off = cache_base + (size_t)(key < len ? key : 0) * D + col * 8;
+    b.k[i] = *(const uint4*)(kc + off);
+    b.v[i] = *(const uint4*)(vc + off);
   }
 }
 
-// Single-pass variant: one workgroup per query head streams every cached key of its
-// kv head through LDS in tiles of KT with an online softmax (running max / sum,
-// accumulator rescaled per tile) -- no cross-workgroup combine, so no device-scope
-// fences.  The next tile's K/V loads are issued before the current tile is computed.
-// The workgroup of the kv head's first query head writes the new key/value to the
-// cache; the others use their own identical copy for that row.
+template <int D>
+__device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int len, int pos, int wave, int krow,
+                                             int col, const float (&qv)[8], const uint16_t* s_knew,
+                                             const uint16_t* s_vnew, float scale, float& m_run, float& l_run,
+                                             float (&acc)[8]) {
+  using T = AttnTile<D>;
+  float s[T::P];
+  float m_tile = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < T::P; ++i) {
+    const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
+    const uint4 kr = key == pos ? *(const uint4*)(s_knew + col * 8) : b.k[i];
+    const uint32_t w[4] = {kr.x, kr.y, kr.z, kr.w};
+    float d = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      d = fmaf(qv[2 * u + 1], bf16_bits_to_f32(w[u] >> 16), fmaf(qv[2 * u], bf16_bits_to_f32(w[u] & 0xffffu), d));
+#pragma unroll
+    for (int off = 1; off < T::LPK; off <<= 1) d += __shfl_xor(d, off, 64);
+    s[i] = key < len ? d * scale : -INFINITY;
+    m_tile = fmaxf(m_tile, s[i]);
+  }
+#pragma unroll
+  for (int off = T::LPK; off < 64; off <<= 1) m_tile = fmaxf(m_tile, __shfl_xor(m_tile, off, 64));
+  const float m_new = fmaxf(m_run, m_tile);
+  if (m_new == -INFINITY) return;  // no valid key for this wave yet
+  const float alpha = expf(m_run - m_new);  // 0 while m_run is -inf
+  l_run *= alpha;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+  for (int i = 0; i < T::P; ++i) {
+    const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
+    const float p = s[i] == -INFINITY ? 0.0f : expf(s[i] - m_new);
+    l_run += p;
+    const uint4 vr = key == pos ? *(const uint4*)(s_vnew + col * 8) : b.v[i];
+    const uint32_t w[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[2 * u] = fmaf(p, bf16_bits_to_f32(w[u] & 0xffffu), acc[2 * u]);
+      acc[2 * u + 1] = fmaf(p, bf16_bits_to_f32(w[u] >> 16), acc[2 * u + 1]);
+    }
+  }
+  m_run = m_new;
+}
+
 template <int D, int OUT>
-__global__ __launch_bounds__(256) void attn_single_kernel(
+__global__ __launch_bounds__(1024) void attn_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
     int max_seq, float scale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
     float* __restrict__ out_s) {
-  constexpr int NT = 256;
-  constexpr int KT = attn_chunk(D);
+  using T = AttnTile<D>;
   constexpr int HALF = D / 2;
-  constexpr int ROW = D + 8;
-  constexpr int U4_ROW = D / 8;
-  constexpr int U4_T = KT * U4_ROW / NT;
-  constexpr int TPK = NT / KT;
-  constexpr int DPT = D / TPK;
-  constexpr int DP = D / 2;
-  constexpr int KG = NT / DP;
-  constexpr int KPG = KT / KG;
-  static_assert(U4_T * NT == KT * U4_ROW && DPT % 8 == 0 && KG * DP == NT, "attention tiling");
-
-  __shared__ __align__(16) uint16_t s_k[KT * ROW];
-  __shared__ __align__(16) uint16_t s_v[KT * ROW];
   __shared__ float s_q[D];
   __shared__ __align__(16) uint16_t s_knew[D];
   __shared__ __align__(16) uint16_t s_vnew[D];
-  __shared__ float s_p[KT];
-  __shared__ float s_wm[NT / 64];
-  __shared__ float s_wl[NT / 64];
-  __shared__ float s_red[KG * D];
+  __shared__ float s_m[T::NW], s_l[T::NW];
+  __shared__ float s_acc[T::NW * D];
 
   const int hq = blockIdx.x;
   const int G = num_heads / num_kv_heads;
   const int kvh = hq / G;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int pos = min(max(*d_pos, 0), max_seq - 1);  // clamped like the split kernel
+  const int wave = tid >> 6, lane = tid & 63;
+  const int col = lane % T::LPK, krow = lane / T::LPK;
+  // a position past the cache is clamped to its last slot (the host bounds the step
+  // count; the clamp only keeps every access inside the cache and the RoPE tables)
+  const int pos = min(max(*d_pos, 0), max_seq - 1);
   const int len = pos + 1;
-  const int ntiles = (len + KT - 1) / KT;
+  const int ntiles = (len + T::KT - 1) / T::KT;
   const size_t cache_base = (size_t)kvh * max_seq * D;
 
-  uint4 rk[U4_T], rv[U4_T];
-  auto issue = [&](int t) {
-    const int t0 = t * KT;
-#pragma unroll
-    for (int i = 0; i < U4_T; ++i) {
-      const int piece = tid + i * NT;
-      const int row = piece / U4_ROW, col = piece % U4_ROW;
-      const int tr = t0 + row < len ? t0 + row : t0;
-      const size_t off = cache_base + (size_t)tr * D + col * 8;
-      rk[i] = *(const uint4*)(kc + off);
-      rv[i] = *(const uint4*)(vc + off);
-    }
-  };
-  issue(0);
+  AttnTile<D> b0, b1;
+  attn_issue<D>(b0, kc, vc, cache_base, 0, len, wave, krow, col);
 
   const float* cs = rope_cos + (size_t)pos * HALF;
   const float* sn = rope_sin + (size_t)pos * HALF;
-  for (int i = tid; i < HALF; i += NT) {
+  for (int i = tid; i < HALF; i += 1024) {
     const float* qh = q + (size_t)hq * D;
     const float q0 = qh[i], q1 = qh[i + HALF];
     s_q[i] = q0 * cs[i] - q1 * sn[i];
@@ -439,100 +203,65 @@ __global__ __launch_bounds__(256) void attn_single_kernel(
     s_knew[i] = f32_to_bf16_bits(k0 * cs[i] - k1 * sn[i]);
     s_knew[i + HALF] = f32_to_bf16_bits(k0 * sn[i] + k1 * cs[i]);
   }
-  for (int i = tid; i < D; i += NT) s_vnew[i] = f32_to_bf16_bits(v[(size_t)kvh * D + i]);
+  for (int i = tid; i < D; i += 1024) s_vnew[i] = f32_to_bf16_bits(v[(size_t)kvh * D + i]);
   lds_barrier();
   if (hq % G == 0)
-    for (int i = tid; i < D; i += NT) {
+    for (int i = tid; i < D; i += 1024) {
       kc[cache_base + (size_t)pos * D + i] = s_knew[i];
       vc[cache_base + (size_t)pos * D + i] = s_vnew[i];
     }
+  float qv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) qv[e] = s_q[col * 8 + e];
 
-  float m_run = -INFINITY, l_run = 0.0f;
-  const int dp = tid % DP, kg = tid / DP;
-  float a0 = 0.0f, a1 = 0.0f;
-  const int j = tid / TPK, r = tid % TPK;
-  for (int t = 0; t < ntiles; ++t) {
-    const int t0 = t * KT;
-    const int prow = pos - t0;  // row of the new token in this tile (if < KT)
+  float m_run = -INFINITY, l_run = 0.0f, acc[8];
 #pragma unroll
-    for (int i = 0; i < U4_T; ++i) {
-      const int piece = tid + i * NT;
-      const int row = piece / U4_ROW, col = piece % U4_ROW;
-      uint4 a = rk[i], b = rv[i];
-      if (row == prow) {
-        a = *(const uint4*)(s_knew + col * 8);
-        b = *(const uint4*)(s_vnew + col * 8);
-      }
-      *(uint4*)(s_k + row * ROW + col * 8) = a;
-      *(uint4*)(s_v + row * ROW + col * 8) = b;
-    }
-    lds_barrier();
-    if (t + 1 < ntiles) issue(t + 1);
-    // scores
-    float s = 0.0f;
-#pragma unroll
-    for (int d0 = 0; d0 < DPT; d0 += 8) {
-      const uint4 raw = *(const uint4*)(s_k + j * ROW + r * DPT + d0);
-      const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int u2 = 0; u2 < 4; ++u2) {
-        const int dd = r * DPT + d0 + 2 * u2;
-        s = fmaf(s_q[dd + 1], bf16_bits_to_f32(wv[u2] >> 16), fmaf(s_q[dd], bf16_bits_to_f32(wv[u2] & 0xffffu), s));
-      }
-    }
-#pragma unroll
-    for (int off = 1; off < TPK; off <<= 1) s += __shfl_xor(s, off, 64);
-    const bool valid = t0 + j < len;
-    s = valid ? s * scale : -INFINITY;
-    float mw = s;
-    for (int off = 32; off > 0; off >>= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
-    if ((tid & 63) == 0) s_wm[wave] = mw;
-    lds_barrier();
-    float m_tile = s_wm[0];
-#pragma unroll
-    for (int w = 1; w < NT / 64; ++w) m_tile = fmaxf(m_tile, s_wm[w]);
-    const float m_new = fmaxf(m_run, m_tile);
-    const float p = valid ? expf(s - m_new) : 0.0f;
-    if (r == 0) s_p[j] = p;
-    float lw = r == 0 ? p : 0.0f;
-    for (int off = 32; off > 0; off >>= 1) lw += __shfl_xor(lw, off, 64);
-    if ((tid & 63) == 0) s_wl[wave] = lw;
-    lds_barrier();
-    const float alpha = expf(m_run - m_new);  // 0 on the first tile
-    float lt = s_wl[0];
-#pragma unroll
-    for (int w = 1; w < NT / 64; ++w) lt += s_wl[w];
-    l_run = fmaf(l_run, alpha, lt);
-    a0 *= alpha;
-    a1 *= alpha;
-#pragma unroll 4
-    for (int jj = 0; jj < KPG; ++jj) {
-      const int jv = kg * KPG + jj;
-      const uint32_t w2 = *(const uint32_t*)(s_v + jv * ROW + 2 * dp);
-      const float pv = s_p[jv];
-      a0 = fmaf(pv, bf16_bits_to_f32(w2 & 0xffffu), a0);
-      a1 = fmaf(pv, bf16_bits_to_f32(w2 >> 16), a1);
-    }
-    m_run = m_new;
-    lds_barrier();  // tile buffers, s_p and s_wm / s_wl are rewritten next
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  // double-buffered tiles; the loads are unconditional (the last tile is re-read past
+  // the end) so the compiler's wait for one buffer never covers the other
+  const int last = ntiles - 1;
+  for (int t = 0; t < ntiles; t += 2) {
+    attn_issue<D>(b1, kc, vc, cache_base, min(t + 1, last), len, wave, krow, col);
+    attn_compute<D>(b0, t, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
+    attn_issue<D>(b0, kc, vc, cache_base, min(t + 2, last), len, wave, krow, col);
+    if (t + 1 < ntiles)
+      attn_compute<D>(b1, t + 1, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
   }
-  s_red[kg * D + 2 * dp] = a0;
-  s_red[kg * D + 2 * dp + 1] = a1;
+  // merge the rows of the wave (same columns), then the waves through LDS
+#pragma unroll
+  for (int off = T::LPK; off < 64; off <<= 1) {
+    l_run += __shfl_xor(l_run, off, 64);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
+  }
+  if (krow == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_acc[wave * D + col * 8 + e] = acc[e];
+    if (col == 0) {
+      s_m[wave] = m_run;
+      s_l[wave] = l_run;
+    }
+  }
   lds_barrier();
   if (tid < D / 4) {
-    const float invL = 1.0f / l_run;
-    float o[4];
+    float M = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      float a = 0.0f;
+    for (int w = 0; w < T::NW; ++w) M = fmaxf(M, s_m[w]);
+    float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int g2 = 0; g2 < KG; ++g2) a += s_red[g2 * D + 4 * tid + t];
-      o[t] = a * invL;
+    for (int w = 0; w < T::NW; ++w) {
+      const float f = s_m[w] == -INFINITY ? 0.0f : expf(s_m[w] - M);
+      L = fmaf(f, s_l[w], L);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = fmaf(f, s_acc[w * D + 4 * tid + e], o[e]);
     }
+    const float invL = 1.0f / L;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] *= invL;
     const size_t i0 = (size_t)hq * D + 4 * tid;
     if (OUT == 1) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) out_bf16[i0 + t] = f32_to_bf16_bits(o[t]);
+      for (int e = 0; e < 4; ++e) out_bf16[i0 + e] = f32_to_bf16_bits(o[e]);
     } else {
       q8_group8_store(o, true, out_q, out_s, i0);
     }
@@ -648,14 +377,13 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
 namespace nve_host {
 
 struct DecodeWs {
-  int* counters;       // [num_kv_heads] attention arrival counters, then [1] argmax (zero at rest)
+  int* counters;       // [1] argmax arrival counter (zero at rest)
   uint16_t* act_bf16;  // [max(H, Hq*D, F)]
   int8_t* xq;          // [max(H, Hq*D, F)]
   float* xs;           // [max/32]
   float* q;            // [Hq*D]
   float* k;            // [Hkv*D]
   float* v;            // [Hkv*D]
-  float* part;         // [Hq * nchunk * (D+2)] attention partials
   float* gate;         // [F]
   float* up;           // [F]
   float* arg_v;        // [kArgmaxBlocks]
@@ -666,18 +394,12 @@ struct DecodeWs {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static int attn_nchunk(const nve_decode_config& c) {
-  const int kc = nve::attn_chunk(c.head_dim);
-  return (c.max_seq + kc - 1) / kc;
-}
-
 static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
   DecodeWs w{};
   const size_t qd = (size_t)c.num_heads * c.head_dim, kd = (size_t)c.num_kv_heads * c.head_dim;
   size_t mx = (size_t)c.hidden;
   if (qd > mx) mx = qd;
   if ((size_t)c.ffn > mx) mx = c.ffn;
-  const size_t nchunk = attn_nchunk(c);
   char* p = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -685,14 +407,13 @@ static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
     off += align256(bytes);
     return r;
   };
-  w.counters = (int*)take(((size_t)c.num_kv_heads + 1) * 4);
+  w.counters = (int*)take(4);
   w.act_bf16 = (uint16_t*)take(mx * 2);
   w.xq = (int8_t*)take(mx);
   w.xs = (float*)take(mx / 32 * 4);
   w.q = (float*)take(qd * 4);
   w.k = (float*)take(kd * 4);
   w.v = (float*)take(kd * 4);
-  w.part = (float*)take((size_t)c.num_heads * nchunk * (c.head_dim + 2) * 4);
   w.gate = (float*)take((size_t)c.ffn * 4);
   w.up = (float*)take((size_t)c.ffn * 4);
   w.arg_v = (float*)take(nve::kArgmaxBlocks * 4);
@@ -710,7 +431,7 @@ static int check_cfg(const nve_decode_config& c) {
       c.ffn < 32 || c.ffn % 32 || c.max_seq < 1 || ((size_t)c.num_heads * c.head_dim) % 32)
     return NVE_ERR_SHAPE;
   if (c.hidden > NVE_MAX_K || c.ffn > NVE_MAX_K || c.num_heads * c.head_dim > NVE_MAX_K ||
-      attn_nchunk(c) > nve::kAttnMaxChunks)
+      (size_t)c.num_kv_heads * c.max_seq * c.head_dim > (size_t)INT32_MAX)
     return NVE_ERR_TOO_LARGE;
   return NVE_OK;
 }
@@ -756,24 +477,13 @@ static hipError_t launch_rmsnorm(const nve_decode_config& c, const float* h, con
   return hipGetLastError();
 }
 
-// Longest cache served by the single-pass attention kernel; longer caches use the
-// split-sequence kernel.
-constexpr int kAttnSinglePassMax = 8192;
-
 static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_io& io, const DecodeWs& ws,
                                    bool w4a8, hipStream_t s) {
   const float scale = 1.0f / sqrtf((float)c.head_dim);
-  const bool single = c.max_seq <= kAttnSinglePassMax;
-  const dim3 grid(c.num_kv_heads, attn_nchunk(c));
-#define NVE_ATTN(D, OUT)                                                                                         \
-  if (single)                                                                                                    \
-    hipLaunchKernelGGL((nve::attn_single_kernel<D, OUT>), dim3(c.num_heads), dim3(256), 0, s, ws.q, ws.k, ws.v,  \
-                       io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads, c.num_kv_heads,   \
-                       c.max_seq, scale, ws.act_bf16, ws.xq, ws.xs);                                            \
-  else                                                                                                           \
-    hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT>), grid, dim3(256), 0, s, ws.q, ws.k, ws.v, io.k_cache,   \
-                       io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads, c.num_kv_heads, c.max_seq,    \
-                       scale, ws.part, ws.counters, ws.act_bf16, ws.xq, ws.xs)
+#define NVE_ATTN(D, OUT)                                                                                       \
+  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT>), dim3(c.num_heads), dim3(1024), 0, s, ws.q, ws.k, ws.v, \
+                     io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads, c.num_kv_heads,   \
+                     c.max_seq, scale, ws.act_bf16, ws.xq, ws.xs)
   if (c.head_dim == 64) {
     if (w4a8) NVE_ATTN(64, 2); else NVE_ATTN(64, 1);
   } else if (c.head_dim == 128) {
@@ -785,49 +495,76 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
   return hipGetLastError();
 }
 
+// Fused producers in the decode layer (RMSNorm into Q/K/V and gate/up, SiLU * up into
+// down); NVE_DECODE_FUSE=0 (read at every call, so a host can switch per call) selects
+// the standalone producer kernels instead.
+static bool decode_fuse() {
+  const char* e = getenv("NVE_DECODE_FUSE");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
+static hipError_t gemv(bool w4a8, const DecodeWs& ws, const W4Segs& sg, int out_dt, int K, hipStream_t s) {
+  return w4a8 ? launch_w4a8(ws.xq, ws.xs, sg, out_dt, K, s)
+              : launch_w4a16(ws.act_bf16, NVE_DT_BF16, sg, out_dt, K, s);
+}
+
+static hipError_t gemv_fused(bool w4a8, int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& sg, int out_dt,
+                             int K, hipStream_t s) {
+  return w4a8 ? launch_w4a8_fused(src, swiglu, pa, sg, out_dt, K, s)
+              : launch_w4a16_fused(src, swiglu, pa, sg, out_dt, K, s);
+}
+
 int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                          bool w4a8, hipStream_t s) {
   const DecodeWs ws = layout_ws(c, io.workspace);
   const int H = c.hidden, F = c.ffn, QD = c.num_heads * c.head_dim;
+  const bool fuse = decode_fuse();
   // attention sub-layer: norm -> Q/K/V (one grouped launch) -> attention -> o_proj (+h)
-  NVE_TRY(launch_rmsnorm(c, io.hidden, w.input_norm, w4a8, ws, s));
   {
     const nve_w4_weight qkv[3] = {w.q, w.k, w.v};
     void* outs[3] = {ws.q, ws.k, ws.v};
     const W4Segs sg = segs3(qkv, outs, 3);
-    if (w4a8)
-      NVE_TRY(launch_w4a8(ws.xq, ws.xs, sg, NVE_DT_F32, H, s));
-    else
-      NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, sg, NVE_DT_F32, H, s));
+    if (fuse) {
+      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, false, nve::ProdArgs{io.hidden, w.input_norm, c.eps}, sg, NVE_DT_F32,
+                         H, s));
+    } else {
+      NVE_TRY(launch_rmsnorm(c, io.hidden, w.input_norm, w4a8, ws, s));
+      NVE_TRY(gemv(w4a8, ws, sg, NVE_DT_F32, H, s));
+    }
   }
   // attention writes the o_proj input directly (int8 + scales, or bf16)
   NVE_TRY(launch_attention(c, io, ws, w4a8, s));
-  if (w4a8)
-    NVE_TRY(launch_w4a8(ws.xq, ws.xs, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
-  else
-    NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
-  // FFN sub-layer: norm -> gate/up (one grouped launch) -> silu*up -> down (+h)
-  NVE_TRY(launch_rmsnorm(c, io.hidden, w.post_attn_norm, w4a8, ws, s));
+  NVE_TRY(gemv(w4a8, ws, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
+  // FFN sub-layer: norm -> gate/up (one grouped launch) -> silu*up -> down (+h).  Fused:
+  // the gate/up launch pairs the rows of both matrices and writes silu(gate) * up
+  // (f32 for W4A8, whose down GEMV quantizes it in its staging; bf16 for W4A16).
   {
     const nve_w4_weight gu[2] = {w.gate, w.up};
+    if (fuse) {
+      void* outs[2] = {w4a8 ? (void*)ws.gate : (void*)ws.act_bf16, nullptr};
+      const W4Segs sg = segs3(gu, outs, 2);
+      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, true, nve::ProdArgs{io.hidden, w.post_attn_norm, c.eps}, sg,
+                         w4a8 ? NVE_DT_F32 : NVE_DT_BF16, H, s));
+      if (w4a8)
+        NVE_TRY(gemv_fused(true, nve::SRC_F32, false, nve::ProdArgs{ws.gate, nullptr, 0.0f},
+                           one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
+      else
+        NVE_TRY(gemv(false, ws, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
+      return NVE_OK;
+    }
     void* outs[2] = {ws.gate, ws.up};
     const W4Segs sg = segs3(gu, outs, 2);
-    if (w4a8)
-      NVE_TRY(launch_w4a8(ws.xq, ws.xs, sg, NVE_DT_F32, H, s));
-    else
-      NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, sg, NVE_DT_F32, H, s));
+    NVE_TRY(launch_rmsnorm(c, io.hidden, w.post_attn_norm, w4a8, ws, s));
+    NVE_TRY(gemv(w4a8, ws, sg, NVE_DT_F32, H, s));
   }
   const dim3 sgrid((F / 4 + 255) / 256);
-  if (w4a8) {
+  if (w4a8)
     hipLaunchKernelGGL(nve::silu_mul_kernel<1>, sgrid, dim3(256), 0, s, ws.gate, ws.up, F, nullptr, ws.xq, ws.xs);
-    NVE_TRY(hipGetLastError());
-    NVE_TRY(launch_w4a8(ws.xq, ws.xs, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
-  } else {
+  else
     hipLaunchKernelGGL(nve::silu_mul_kernel<0>, sgrid, dim3(256), 0, s, ws.gate, ws.up, F, ws.act_bf16, nullptr,
                        nullptr);
-    NVE_TRY(hipGetLastError());
-    NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
-  }
+  NVE_TRY(hipGetLastError());
+  NVE_TRY(gemv(w4a8, ws, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
   return NVE_OK;
 }
 
@@ -841,7 +578,7 @@ int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8
     NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
   hipLaunchKernelGGL(nve::argmax_embed_kernel, dim3(nve::kArgmaxBlocks), dim3(256), 0, s, logits, hd.lm_head.n,
                      hd.embed, c.hidden, hd.hidden, hd.token_out, hd.pos, ws.arg_v, ws.arg_i,
-                     ws.counters + c.num_kv_heads);
+                     ws.counters);
   return (int)hipGetLastError();
 }
 

@@ -31,13 +31,22 @@
 #include "common.h"
 #include "w4_launch.h"
 
+#include "act_producer.h"
 #include "w4a16_ops.h"
 
 namespace nve {
 
-template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI>
+// SRC != SRC_PLAIN (MODE_BF16 only): the activations are computed in the staging
+// from the producer's inputs (act_producer.h) and rounded to bf16.
+// SWI: SwiGLU pairing -- segment 0 (gate) and the matrix in nib[1] / sc[1] (up)
+// share N; a wave computes R/2 rows of each and writes silu(gate) * up
+// (src/ops.rs:62-64) for its R/2 rows.
+template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, bool SWI = false>
 __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict__ x, W4Segs segs,
-                                                         int K) {
+                                                         int K, ProdArgs pa) {
+  static_assert(SRC == SRC_PLAIN || (!MULTI && MODE == MODE_BF16), "fused producers: one-pass bf16 staging");
+  static_assert(!SWI || (R % 2 == 0 && !MULTI && MODE != MODE_F32), "SwiGLU pairing: even R, one pass");
+  constexpr int RH = SWI ? R / 2 : R;  // output rows per wave
   constexpr int SPT = NJ;  // staging passes: K/8 chunks <= 256*NJ
   extern __shared__ int4 lds[];
   const int nb = K >> 5;
@@ -57,13 +66,17 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   void* __restrict__ out = sg == 0 ? segs.out[0] : (sg == 1 ? segs.out[1] : segs.out[2]);
   const int N = sg == 0 ? segs.n[0] : (sg == 1 ? segs.n[1] : segs.n[2]);
   const int wg0 = sg == 0 ? 0 : (sg == 1 ? segs.wg_begin[1] : segs.wg_begin[2]);
-  const int row0 = ((wg - wg0) * 4 + wave) * R;
+  const int row0 = ((wg - wg0) * 4 + wave) * RH;
   const uint4* __restrict__ x4 = (const uint4*)x;
 
   // (1) activation staging loads (clamped index, unconditional)
-  uint4 stv[SPT];
+  uint4 stv[SRC == SRC_PLAIN ? SPT : 1];
   float4 sta0[MODE == MODE_F32 ? SPT : 1], sta1[MODE == MODE_F32 ? SPT : 1];
-  if (!MULTI) {
+  ProdChunk<SRC, 8> pc[SRC == SRC_PLAIN ? 1 : SPT];
+  if constexpr (SRC != SRC_PLAIN) {
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) prod_issue<SRC, 8>(pc[s], pa, (int)threadIdx.x + 256 * s, nchunk);
+  } else if (!MULTI) {
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = min((int)threadIdx.x + 256 * s, nchunk - 1);
@@ -88,9 +101,11 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   auto issue = [&](int jb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, N - 1);
-      const uint4* rn = (const uint4*)(nib + (size_t)row * row_bytes);
-      const float* rs = ws + (size_t)row * nb;
+      const int row = min(row0 + (SWI ? r % RH : r), N - 1);
+      const uint8_t* mn = (SWI && r >= RH) ? segs.nib[1] : nib;
+      const float* ms = (SWI && r >= RH) ? segs.sc[1] : ws;
+      const uint4* rn = (const uint4*)(mn + (size_t)row * row_bytes);
+      const float* rs = ms + (size_t)row * nb;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int bb = min(jb + lane + 64 * j, nb - 1);
@@ -103,7 +118,19 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   __builtin_amdgcn_sched_barrier(0);
 
   // (3) LDS writes
-  if (!MULTI) {
+  if constexpr (SRC != SRC_PLAIN) {
+    double inv = 0.0;
+    if (SRC == SRC_NORM)
+      inv = prod_norm_inv(prod_sumsq<SRC, 8, SPT>(pc, nchunk), K, pa.eps,
+                          (double*)((char*)lds + w4a16_lds_bytes(MODE, K)));
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = (int)threadIdx.x + 256 * s;
+      float v[8];
+      prod_values<SRC, 8>(pc[s], inv, v);
+      w4a16_stage_put_dot<MODE>(prod_bf16x8(v), i, i < nchunk, nb, s_p, s_mul);
+    }
+  } else if (!MULTI) {
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;
@@ -153,10 +180,19 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
     issue(jb);
   }
 
+  if constexpr (SWI) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float v = wave_sum_to_lane63(acc[r]);
-    if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+    for (int r = 0; r < RH; ++r) {
+      const float g = wave_sum_to_lane63(acc[r]);
+      const float u = wave_sum_to_lane63(acc[r + RH]);
+      if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), g / (1.0f + expf(-g)) * u);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum_to_lane63(acc[r]);
+      if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+    }
   }
 }
 
@@ -167,15 +203,16 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
 // ---------------------------------------------------------------------------
 namespace nve_host {
 
-template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI>
-static hipError_t launch_w4a16_t(const void* x, const W4Segs& segs, int K, hipStream_t stream) {
-  const size_t lds = nve::w4a16_lds_bytes(MODE, K);
-  auto kern = nve::w4a16_gemv_kernel<MODE, XDT, OUT_DT, R, NJ, MULTI>;
+template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = nve::SRC_PLAIN, bool SWI = false>
+static hipError_t launch_w4a16_t(const void* x, const W4Segs& segs, int K, hipStream_t stream,
+                                 const nve::ProdArgs& pa = nve::ProdArgs{}) {
+  const size_t lds = nve::w4a16_lds_bytes(MODE, K) + (SRC == nve::SRC_NORM ? 64 : 0);
+  auto kern = nve::w4a16_gemv_kernel<MODE, XDT, OUT_DT, R, NJ, MULTI, SRC, SWI>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(segs.wg_total), dim3(256), lds, stream, x, segs, K);
+  hipLaunchKernelGGL(kern, dim3(segs.wg_total), dim3(256), lds, stream, x, segs, K, pa);
   return hipGetLastError();
 }
 
@@ -186,6 +223,30 @@ static hipError_t launch_w4a16_m(const void* x, W4Segs segs, int K, hipStream_t 
 #define NVE_W4A16_CASE(RR, JJ, MM) \
   if (t.R == RR && t.NJ == JJ && t.multi == MM) \
     return launch_w4a16_t<MODE, XDT, OUT_DT, RR, JJ, MM>(x, segs, K, stream);
+  NVE_W4_TILING_CASES(NVE_W4A16_CASE)
+#undef NVE_W4A16_CASE
+  return hipErrorInvalidValue;
+}
+
+template <int OUT_DT, int SRC, bool SWI>
+static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream) {
+  const W4Tiling t = choose_w4_tiling(segs, K);
+  if (t.multi) return hipErrorInvalidValue;
+  if (SWI) {
+    const int R = t.R < 2 ? 2 : t.R;
+    segs.nseg = 1;  // gate in slot 0, up in slot 1 (read by the kernel directly)
+    finalize_segments(segs, R / 2);
+#define NVE_W4A16_SWI_CASE(RR, JJ) \
+    if (R == RR && t.NJ == JJ) \
+      return launch_w4a16_t<nve::MODE_BF16, NVE_DT_BF16, OUT_DT, RR, JJ, false, SRC, true>(nullptr, segs, K, stream, pa);
+    NVE_W4_SWIGLU_CASES(NVE_W4A16_SWI_CASE)
+#undef NVE_W4A16_SWI_CASE
+    return hipErrorInvalidValue;
+  }
+  finalize_segments(segs, t.R);
+#define NVE_W4A16_CASE(RR, JJ, MM) \
+  if (t.R == RR && t.NJ == JJ && !MM) \
+    return launch_w4a16_t<nve::MODE_BF16, NVE_DT_BF16, OUT_DT, RR, JJ, false, SRC>(nullptr, segs, K, stream, pa);
   NVE_W4_TILING_CASES(NVE_W4A16_CASE)
 #undef NVE_W4A16_CASE
   return hipErrorInvalidValue;
@@ -216,6 +277,18 @@ hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt,
     case NVE_DT_F32_ACCUM: return launch_w4a16_o<NVE_DT_F32_ACCUM>(x, x_dt, segs, K, stream);
     default: return launch_w4a16_o<NVE_DT_F32>(x, x_dt, segs, K, stream);
   }
+}
+
+// Decode-layer W4A16 GEMVs with a fused producer (act_producer.h), bf16 staging:
+//   NORM, F32          Q/K/V from the residual and the norm weights;
+//   NORM, BF16, swiglu gate/up -> silu(gate) * up rounded to bf16 (the down input).
+hipError_t launch_w4a16_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                              hipStream_t stream) {
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && !swiglu)
+    return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, false>(pa, segs, K, stream);
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_BF16 && swiglu)
+    return launch_w4a16_fused_t<NVE_DT_BF16, nve::SRC_NORM, true>(pa, segs, K, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace nve_host

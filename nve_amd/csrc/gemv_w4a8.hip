@@ -27,16 +27,25 @@
 #include "common.h"
 #include "w4_launch.h"
 
+#include "act_producer.h"
 #include "w4a8_ops.h"
 
 namespace nve {
 
 // R rows per wave, NJ 64-block chunks per lane in registers.  MULTI = K needs more
-// than one pass of NJ chunks (K > 64*NJ*32); then staging runs as a loop.
-template <int OUT_DT, int R, int NJ, bool MULTI>
+// than one pass of NJ chunks (K > 64*NJ*32); then staging runs as a loop.  SRC !=
+// SRC_PLAIN computes the activations in the staging from the producer's inputs
+// (act_producer.h) and quantizes them in place of reading xq / xs.
+// SWI: SwiGLU pairing -- segment 0 (gate) and the matrix in nib[1] / sc[1] (up)
+// share N; a wave computes R/2 rows of each and writes silu(gate) * up
+// (src/ops.rs:62-64) for its R/2 rows.
+template <int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, bool SWI = false>
 __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xs,
-                                                        W4Segs segs, int K) {
+                                                        W4Segs segs, int K, ProdArgs pa) {
+  static_assert(SRC == SRC_PLAIN || !MULTI, "fused producers stage in one pass");
+  static_assert(!SWI || (R % 2 == 0 && !MULTI), "SwiGLU pairing: even R, one pass");
+  constexpr int RH = SWI ? R / 2 : R;  // output rows per wave
   constexpr int SPT = (NJ + 1) / 2;  // staging passes: 2*nb <= 128*NJ chunks of 16 B
   extern __shared__ int4 lds[];
   const int nb = K >> 5;
@@ -55,10 +64,16 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   void* __restrict__ out = sg == 0 ? segs.out[0] : (sg == 1 ? segs.out[1] : segs.out[2]);
   const int N = sg == 0 ? segs.n[0] : (sg == 1 ? segs.n[1] : segs.n[2]);
   const int wg0 = sg == 0 ? 0 : (sg == 1 ? segs.wg_begin[1] : segs.wg_begin[2]);
-  const int row0 = ((wg - wg0) * 4 + wave) * R;
+  const int row0 = ((wg - wg0) * 4 + wave) * RH;
 
-  W4A8Stage<SPT> st;
-  if (!MULTI) w4a8_stage_issue<SPT>(st, xq, xs, nchunk);
+  W4A8Stage<SRC == SRC_PLAIN ? SPT : 1> st;
+  ProdChunk<SRC, 16> pc[SRC == SRC_PLAIN ? 1 : SPT];
+  if constexpr (SRC != SRC_PLAIN) {
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) prod_issue<SRC, 16>(pc[s], pa, (int)threadIdx.x + 256 * s, nchunk);
+  } else if (!MULTI) {
+    w4a8_stage_issue<SPT>(st, xq, xs, nchunk);
+  }
   // Keep the issue order: staging loads, then weight loads, then LDS writes (which
   // then wait only for the older staging loads).
   __builtin_amdgcn_sched_barrier(0);
@@ -71,9 +86,11 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   auto issue = [&](int jb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, N - 1);
-      const uint4* rn = (const uint4*)(nib + (size_t)row * row_bytes);
-      const float* rs = ws + (size_t)row * nb;
+      const int row = min(row0 + (SWI ? r % RH : r), N - 1);
+      const uint8_t* mn = (SWI && r >= RH) ? segs.nib[1] : nib;
+      const float* ms = (SWI && r >= RH) ? segs.sc[1] : ws;
+      const uint4* rn = (const uint4*)(mn + (size_t)row * row_bytes);
+      const float* rs = ms + (size_t)row * nb;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int b = jb + lane + 64 * j;
@@ -86,10 +103,25 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   issue(0);
   __builtin_amdgcn_sched_barrier(0);
 
-  if (!MULTI)
+  if constexpr (SRC != SRC_PLAIN) {
+    double inv = 0.0;
+    if (SRC == SRC_NORM)
+      inv = prod_norm_inv(prod_sumsq<SRC, 16, SPT>(pc, nchunk), K, pa.eps,
+                          (double*)((char*)lds + w4a8_lds_bytes(K)));
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = (int)threadIdx.x + 256 * s;
+      float v[16];
+      prod_values<SRC, 16>(pc[s], inv, v);
+      float scale;
+      const int4 q = prod_quant16(v, scale);
+      w4a8_stage_put(q, scale, i, i < nchunk, nb, s_lo, s_hi, s_bs);
+    }
+  } else if (!MULTI) {
     w4a8_stage_write<SPT>(st, s_lo, s_hi, s_bs, nchunk);
-  else
+  } else {
     w4a8_stage_loop(xq, xs, s_lo, s_hi, s_bs, nchunk);
+  }
   lds_barrier();
 
   float acc[R];
@@ -118,10 +150,19 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     issue(jb);
   }
 
+  if constexpr (SWI) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float v = wave_sum_to_lane63(acc[r]);
-    if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+    for (int r = 0; r < RH; ++r) {
+      const float g = wave_sum_to_lane63(acc[r]);
+      const float u = wave_sum_to_lane63(acc[r + RH]);
+      if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), g / (1.0f + expf(-g)) * u);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum_to_lane63(acc[r]);
+      if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+    }
   }
 }
 
@@ -149,16 +190,16 @@ __global__ __launch_bounds__(256) void w4a8_block_acc_kernel(const int8_t* __res
 // ---------------------------------------------------------------------------
 namespace nve_host {
 
-template <int OUT_DT, int R, int NJ, bool MULTI>
+template <int OUT_DT, int R, int NJ, bool MULTI, int SRC, bool SWI>
 static hipError_t launch_w4a8_t(const int8_t* xq, const float* xs, const W4Segs& segs, int K,
-                                int grid, hipStream_t stream) {
-  const size_t lds = nve::w4a8_lds_bytes(K);
-  auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI>;
+                                int grid, const nve::ProdArgs& pa, hipStream_t stream) {
+  const size_t lds = nve::w4a8_lds_bytes(K) + (SRC == nve::SRC_NORM ? 64 : 0);
+  auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI, SRC, SWI>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, xq, xs, segs, K);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, xq, xs, segs, K, pa);
   return hipGetLastError();
 }
 
@@ -170,7 +211,32 @@ static hipError_t launch_w4a8_dt(const int8_t* xq, const float* xs, W4Segs segs,
   const int grid = segs.wg_total;
 #define NVE_W4A8_CASE(RR, JJ, MM) \
   if (t.R == RR && t.NJ == JJ && t.multi == MM) \
-    return launch_w4a8_t<OUT_DT, RR, JJ, MM>(xq, xs, segs, K, grid, stream);
+    return launch_w4a8_t<OUT_DT, RR, JJ, MM, nve::SRC_PLAIN, false>(xq, xs, segs, K, grid, nve::ProdArgs{}, stream);
+  NVE_W4_TILING_CASES(NVE_W4A8_CASE)
+#undef NVE_W4A8_CASE
+  return hipErrorInvalidValue;
+}
+
+// Fused-producer launches (one-shot kernels, one staging pass: K <= 16384).
+template <int OUT_DT, int SRC, bool SWI>
+static hipError_t launch_w4a8_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream) {
+  const W4Tiling t = choose_w4_tiling(segs, K);
+  if (t.multi) return hipErrorInvalidValue;
+  if (SWI) {
+    const int R = t.R < 2 ? 2 : t.R;
+    segs.nseg = 1;  // gate in slot 0, up in slot 1 (read by the kernel directly)
+    finalize_segments(segs, R / 2);
+#define NVE_W4A8_SWI_CASE(RR, JJ) \
+    if (R == RR && t.NJ == JJ) \
+      return launch_w4a8_t<OUT_DT, RR, JJ, false, SRC, true>(nullptr, nullptr, segs, K, segs.wg_total, pa, stream);
+    NVE_W4_SWIGLU_CASES(NVE_W4A8_SWI_CASE)
+#undef NVE_W4A8_SWI_CASE
+    return hipErrorInvalidValue;
+  }
+  finalize_segments(segs, t.R);
+#define NVE_W4A8_CASE(RR, JJ, MM) \
+  if (t.R == RR && t.NJ == JJ && !MM) \
+    return launch_w4a8_t<OUT_DT, RR, JJ, false, SRC, false>(nullptr, nullptr, segs, K, segs.wg_total, pa, stream);
   NVE_W4_TILING_CASES(NVE_W4A8_CASE)
 #undef NVE_W4A8_CASE
   return hipErrorInvalidValue;
@@ -185,6 +251,20 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
     case NVE_DT_F32_ACCUM: return launch_w4a8_dt<NVE_DT_F32_ACCUM>(xq, xs, segs, K, stream);
     default: return launch_w4a8_dt<NVE_DT_F32>(xq, xs, segs, K, stream);
   }
+}
+
+// Decode-layer W4A8 GEMVs with a fused producer (act_producer.h):
+//   NORM, F32          Q/K/V from the residual and the norm weights;
+//   NORM, F32, swiglu  gate/up -> silu(gate) * up (f32);
+//   F32, F32_ACCUM     down from that f32 vector, quantized in the staging.
+hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                             hipStream_t stream) {
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32)
+    return swiglu ? launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, true>(pa, segs, K, stream)
+                  : launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, false>(pa, segs, K, stream);
+  if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
+    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_F32, false>(pa, segs, K, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_w4a8_block_acc(const int8_t* xq, const uint8_t* nib, int32_t* acc, int N, int K,

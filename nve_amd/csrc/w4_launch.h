@@ -58,6 +58,10 @@ inline void finalize_segments(W4Segs& s, int R) {
   X(1, 2, false) X(2, 3, false) X(1, 3, false) X(2, 4, false) X(1, 4, false) X(1, 5, false) \
   X(1, 6, false) X(1, 7, false) X(1, 8, false) X(1, 8, true)
 
+// (R, NJ) pairs of the SwiGLU-paired launches (R even: R/2 gate + R/2 up rows).
+#define NVE_W4_SWIGLU_CASES(X) \
+  X(8, 1) X(4, 1) X(2, 1) X(4, 2) X(2, 2) X(2, 3) X(2, 4) X(2, 5) X(2, 6) X(2, 7) X(2, 8)
+
 // Persistent kernels: R*NJ ~ depth (4 or 8) blocks per lane per buffer, two buffers.
 inline W4Tiling choose_persistent_tiling(int K, int depth) {
   const int nb = K / 32;
@@ -170,6 +174,17 @@ int check_decode(const nve_decode_config& c);
 int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                          bool w4a8, hipStream_t s);
 int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8, hipStream_t s);
+// Fused-producer GEMVs (act_producer.h); swiglu pairs gate (slot 0) with up (nib[1],
+// sc[1]) and writes silu(gate) * up.
+}  // namespace nve_host
+namespace nve {
+struct ProdArgs;
+}
+namespace nve_host {
+hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                             hipStream_t stream);
+hipError_t launch_w4a16_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                              hipStream_t stream);
 hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);

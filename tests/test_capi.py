@@ -109,9 +109,7 @@ def test_decode_argument_errors(L):
     assert call(DecodeConfig(H, hq, hkv, 96, F, 64, 512, 1e-5)) == -2        # head_dim 96
     assert call(DecodeConfig(H, 12, 1, D, F, 64, 512, 1e-5)) == -2           # 12 q heads per kv head
     assert call(DecodeConfig(H + 16, hq, hkv, D, F, 64, 512, 1e-5)) == -2    # H % 32
-    assert call(DecodeConfig(H, hq, hkv, D, F, 16385, 512, 1e-5)) == -5      # cache past the combine's limit
-    assert call(DecodeConfig(H, hq, hkv, 256, F, 8193, 512, 1e-5),
-                weights(q=w(hq * 256, H), k=w(hkv * 256, H), v=w(hkv * 256, H), o=w(H, hq * 256))) == -5
+    assert call(DecodeConfig(H, hq, hkv, D, F, 1 << 26, 512, 1e-5)) == -5    # cache index past int32
     cfg = DecodeConfig(H, hq, hkv, D, F, 64, 512, 1e-5)
     assert call(cfg, weights(gate=w(F, H + 32))) == -2                       # weight shape mismatch
     assert call(cfg, weights(down=W4Weight(None, P16, H, F))) == -1

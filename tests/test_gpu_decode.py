@@ -91,10 +91,14 @@ def _run_teacher_forced(torch, m, steps, token0=5):
     return m
 
 
+@pytest.mark.parametrize("fuse", ["1", "0"])
 @pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256)])
-def test_decode_step_mixed_precision(torch_dev, heads, kv, d):
+def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, monkeypatch):
+    """Both layer paths: producers fused into the GEMV staging, and standalone
+    RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0)."""
+    monkeypatch.setenv("NVE_DECODE_FUSE", fuse)
     m = _model(torch_dev, heads, kv, d)
-    _run_teacher_forced(torch_dev, m, steps=6)  # pos 60..65 crosses the 64-key chunk edge
+    _run_teacher_forced(torch_dev, m, steps=6)  # pos 60..65 crosses a 64-key boundary
 
 
 @pytest.mark.parametrize("importance,lm8", [((0.0, 0.0), True), ((1.0, 1.0), False)])
@@ -131,17 +135,19 @@ def test_decode_graph_replay_matches_eager(torch_dev):
     assert int(m.pos.item()) == 40 + n
 
 
-def test_decode_3b_shape_smoke(torch_dev):
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_decode_3b_shape_smoke(torch_dev, fuse, monkeypatch):
     """The Llama-3.2-3B shapes (head_dim 128, GQA 3, ffn 8192, vocab 128256) on 2 layers:
     one teacher-forced step against the oracle over the full logits."""
+    monkeypatch.setenv("NVE_DECODE_FUSE", fuse)
     from nve_amd.decode import ModelShape, DecodeModel
     s = ModelShape(layers=2)
     m = DecodeModel(s, max_seq=130, prefill=128, importance=np.array([0.0, 1.0]))
     _run_teacher_forced(torch_dev, m, steps=1)
 
 
-def test_decode_split_attention_long_cache(torch_dev):
-    """max_seq above the single-pass limit takes the split-sequence kernel with the
-    cross-workgroup combine; pos 8190..8192 crosses a 64-key chunk edge."""
+def test_decode_long_cache(torch_dev):
+    """A cache of 8190+ keys: many tiles per workgroup (256 keys per tile at head_dim
+    64 -> 32 tiles), pos 8190..8192 crosses a tile edge."""
     m = _model(torch_dev, 4, 2, 64, layers=2, importance=(0.0, 1.0), max_seq=8256, prefill=8190)
     _run_teacher_forced(torch_dev, m, steps=3)
