@@ -192,10 +192,13 @@ int nve_hip_set_gemv_policy(int policy, int persistent_wg_per_cu, int persistent
  * Restates gpu_layer_forward_decode (src/gpu_layer.rs:1005-1084) for one token:
  *   h += o_proj(attn(rope(q), rope(k) ++ K cache, V cache))    with x = rmsnorm(h)
  *   h += down(silu(gate(x2)) * up(x2))                         with x2 = rmsnorm(h)
- * Precision per layer: W4A8 (RMSNorm / SiLU-mul quantize their outputs to int8
- * with group-32 scales, nve_quantize_f16_q8 semantics) or W4A16 (bf16 activations).
- * Q/K/V and gate/up are single grouped launches; residual adds are fused into the
- * o_proj / down GEMVs (NVE_DT_F32_ACCUM).  The position of the token is read from
+ * Precision per layer: W4A8 (every GEMV input quantized to int8 with group-32
+ * scales, nve_quantize_f16_q8 semantics) or W4A16 (bf16 GEMV inputs).  Five launches
+ * per layer: Q/K/V with the RMSNorm computed in its staging; attention (RoPE, cache
+ * append, softmax, output converted to the o_proj input); o_proj with the residual
+ * add; gate/up with the RMSNorm in its staging and silu(gate) * up in its epilogue;
+ * down with the residual add.  (NVE_DECODE_FUSE=0 in the environment selects
+ * standalone RMSNorm / SiLU-mul kernels instead.)  The position of the token is read from
  * device memory (*pos), so a whole step can be captured in a HIP graph and replayed.
  * RMSNorm accumulates in f64 (src/ops.rs:12-30); RoPE pairs (i, i+D/2) with
  * caller-provided cos/sin tables [max_seq, D/2] (src/ops.rs:264-276); attention is
