@@ -58,6 +58,62 @@ __device__ __forceinline__ float quad_max_f(float v) {
   v = fmaxf(v, dpp_mov<0x4E>(v));
   return v;
 }
+// Butterfly across the two 16-lane rows of each 32-lane half (lane l <-> l ^ 16) and
+// across the two halves (l <-> l ^ 32), via v_permlane16_swap / v_permlane32_swap:
+// swapping a value with itself leaves the partner's copy in one of the two results.
+__device__ __forceinline__ float xor16_partner_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ float xor32_partner_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ float xor16_partner_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xor32_partner_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+
+// Sum over aligned groups of N lanes (N = 8, 16, 32 or 64), result in every lane of
+// the group: quad butterflies, then the half-row and row mirrors (a mirror maps one
+// half of the group onto the other), then the permlane swaps.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 8 || N == 16 || N == 32 || N == 64, "group size");
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  if (N >= 16) v += dpp_mov<0x140>(v);  // row_mirror
+  if (N >= 32) v = xor16_partner_sum(v);
+  if (N >= 64) v = xor32_partner_sum(v);
+  return v;
+}
+
+// Sum / max over the lanes l, l ^ S, l ^ 2S, ... (S = 8, 16 or 32): lanes holding the
+// same position within their S-lane group.
+template <int S>
+__device__ __forceinline__ float stride_sum(float v) {
+  static_assert(S == 8 || S == 16 || S == 32, "stride");
+  if (S <= 8) v += dpp_mov<0x128>(v);  // row_ror:8 (lane i <- lane i-8 within its row)
+  if (S <= 16) v = xor16_partner_sum(v);
+  return xor32_partner_sum(v);
+}
+template <int S>
+__device__ __forceinline__ float stride_max(float v) {
+  static_assert(S == 8 || S == 16 || S == 32, "stride");
+  if (S <= 8) v = fmaxf(v, dpp_mov<0x128>(v));
+  if (S <= 16) v = xor16_partner_max(v);
+  return xor32_partner_max(v);
+}
+
 // Pairs of lanes (2i, 2i+1).
 __device__ __forceinline__ int pair_sum_i(int v) { return v + dpp_mov_i<0xB1>(v); }
 

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 // sits in LPK = D/8 consecutive lanes, one piece per lane, so the q.k dot product is
 // a butterfly over those lanes and the value sum accumulates each lane's 8 columns.
 // Every wave keeps its own online softmax (running max m, sum l, accumulator
-// rescaled by e^(m_old - m_new)) over its keys, with the next tile's K/V loads in
+// rescaled by e^(m_old - m_new)) over its keys, with the next two tiles' K/V loads in
 // flight while the current tile is computed; the 16 wave states are merged once in
 // LDS at the end:  out = sum_w e^(m_w - M) acc_w / sum_w e^(m_w - M) l_w.
 // The new token's key is rotated and rounded to bf16 like every cached entry; the
@@ -131,13 +131,11 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       d = fmaf(qv[2 * u + 1], bf16_bits_to_f32(w[u] >> 16), fmaf(qv[2 * u], bf16_bits_to_f32(w[u] & 0xffffu), d));
-#pragma unroll
-    for (int off = 1; off < T::LPK; off <<= 1) d += __shfl_xor(d, off, 64);
+    d = group_sum<T::LPK>(d);
     s[i] = key < len ? d * scale : -INFINITY;
     m_tile = fmaxf(m_tile, s[i]);
   }
-#pragma unroll
-  for (int off = T::LPK; off < 64; off <<= 1) m_tile = fmaxf(m_tile, __shfl_xor(m_tile, off, 64));
+  m_tile = stride_max<T::LPK>(m_tile);
   const float m_new = fmaxf(m_run, m_tile);
   if (m_new == -INFINITY) return;  // no valid key for this wave yet
   const float alpha = expf(m_run - m_new);  // 0 while m_run is -inf
@@ -188,8 +186,14 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   const int ntiles = (len + T::KT - 1) / T::KT;
   const size_t cache_base = (size_t)kvh * max_seq * D;
 
-  AttnTile<D> b0, b1;
+  // three tile buffers in a ring; the first three tiles' loads are issued before the
+  // RoPE phase.  Loads are unconditional (tile indices past the end re-read the last
+  // tile) so the compiler's wait for one buffer never covers a younger one.
+  const int last = ntiles - 1;
+  AttnTile<D> b0, b1, b2;
   attn_issue<D>(b0, kc, vc, cache_base, 0, len, wave, krow, col);
+  attn_issue<D>(b1, kc, vc, cache_base, min(1, last), len, wave, krow, col);
+  attn_issue<D>(b2, kc, vc, cache_base, min(2, last), len, wave, krow, col);
 
   const float* cs = rope_cos + (size_t)pos * HALF;
   const float* sn = rope_sin + (size_t)pos * HALF;
@@ -217,23 +221,20 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   float m_run = -INFINITY, l_run = 0.0f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  // double-buffered tiles; the loads are unconditional (the last tile is re-read past
-  // the end) so the compiler's wait for one buffer never covers the other
-  const int last = ntiles - 1;
-  for (int t = 0; t < ntiles; t += 2) {
-    attn_issue<D>(b1, kc, vc, cache_base, min(t + 1, last), len, wave, krow, col);
+  for (int t = 0; t < ntiles; t += 3) {
     attn_compute<D>(b0, t, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
-    attn_issue<D>(b0, kc, vc, cache_base, min(t + 2, last), len, wave, krow, col);
+    attn_issue<D>(b0, kc, vc, cache_base, min(t + 3, last), len, wave, krow, col);
     if (t + 1 < ntiles)
       attn_compute<D>(b1, t + 1, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
+    attn_issue<D>(b1, kc, vc, cache_base, min(t + 4, last), len, wave, krow, col);
+    if (t + 2 < ntiles)
+      attn_compute<D>(b2, t + 2, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
+    attn_issue<D>(b2, kc, vc, cache_base, min(t + 5, last), len, wave, krow, col);
   }
   // merge the rows of the wave (same columns), then the waves through LDS
+  l_run = stride_sum<T::LPK>(l_run);
 #pragma unroll
-  for (int off = T::LPK; off < 64; off <<= 1) {
-    l_run += __shfl_xor(l_run, off, 64);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
-  }
+  for (int e = 0; e < 8; ++e) acc[e] = stride_sum<T::LPK>(acc[e]);
   if (krow == 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) s_acc[wave * D + col * 8 + e] = acc[e];
