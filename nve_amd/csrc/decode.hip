@@ -100,15 +100,18 @@ struct AttnTile {
   uint4 k[P], v[P];
 };
 
+// Rows past the live length are masked at use, so the load addresses only need to stay
+// below `limit` (max_seq for the first tiles, which are issued before the position is
+// known; the live length afterwards).
 template <int D>
 __device__ __forceinline__ void attn_issue(AttnTile<D>& b, const uint16_t* __restrict__ kc,
-                                           const uint16_t* __restrict__ vc, size_t cache_base, int t, int len,
+                                           const uint16_t* __restrict__ vc, size_t cache_base, int t, int limit,
                                            int wave, int krow, int col) {
   using T = AttnTile<D>;
 #pragma unroll
   for (int i = 0; i < T::P; ++i) {
     const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
-    const size_t off = cache_base + (size_t)(key < len ? key : 0) * D + col * 8;
+    const size_t off = cache_base + (size_t)(key < limit ? key : limit - 1) * D + col * 8;
     b.k[i] = *(const uint4*)(kc + off);
     b.v[i] = *(const uint4*)(vc + off);
   }
@@ -147,7 +150,8 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
     const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
     const float p = s[i] == -INFINITY ? 0.0f : expf(s[i] - m_new);
     l_run += p;
-    const uint4 vr = key == pos ? *(const uint4*)(s_vnew + col * 8) : b.v[i];
+    // rows past the length may hold anything (even NaN): they must not reach acc
+    const uint4 vr = key == pos ? *(const uint4*)(s_vnew + col * 8) : (key < len ? b.v[i] : make_uint4(0, 0, 0, 0));
     const uint32_t w[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -179,35 +183,42 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int col = lane % T::LPK, krow = lane / T::LPK;
+  const size_t cache_base = (size_t)kvh * max_seq * D;
+
+  // three tile buffers in a ring; the first three tiles' loads are issued at once (their
+  // addresses do not depend on the position).  Loads are unconditional (tile indices
+  // past the end re-read the last tile) so the compiler's wait for one buffer never
+  // covers a younger one.
+  AttnTile<D> b0, b1, b2;
+  attn_issue<D>(b0, kc, vc, cache_base, 0, max_seq, wave, krow, col);
+  attn_issue<D>(b1, kc, vc, cache_base, 1, max_seq, wave, krow, col);
+  attn_issue<D>(b2, kc, vc, cache_base, 2, max_seq, wave, krow, col);
+  // q, k, v of this head before the position-dependent RoPE rows
+  float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
+  if (tid < HALF) {
+    q0 = q[(size_t)hq * D + tid];
+    q1 = q[(size_t)hq * D + tid + HALF];
+    k0 = k[(size_t)kvh * D + tid];
+    k1 = k[(size_t)kvh * D + tid + HALF];
+    v0 = v[(size_t)kvh * D + tid];
+    v1 = v[(size_t)kvh * D + tid + HALF];
+  }
   // a position past the cache is clamped to its last slot (the host bounds the step
   // count; the clamp only keeps every access inside the cache and the RoPE tables)
   const int pos = min(max(*d_pos, 0), max_seq - 1);
   const int len = pos + 1;
   const int ntiles = (len + T::KT - 1) / T::KT;
-  const size_t cache_base = (size_t)kvh * max_seq * D;
-
-  // three tile buffers in a ring; the first three tiles' loads are issued before the
-  // RoPE phase.  Loads are unconditional (tile indices past the end re-read the last
-  // tile) so the compiler's wait for one buffer never covers a younger one.
   const int last = ntiles - 1;
-  AttnTile<D> b0, b1, b2;
-  attn_issue<D>(b0, kc, vc, cache_base, 0, len, wave, krow, col);
-  attn_issue<D>(b1, kc, vc, cache_base, min(1, last), len, wave, krow, col);
-  attn_issue<D>(b2, kc, vc, cache_base, min(2, last), len, wave, krow, col);
 
-  const float* cs = rope_cos + (size_t)pos * HALF;
-  const float* sn = rope_sin + (size_t)pos * HALF;
-  for (int i = tid; i < HALF; i += 1024) {
-    const float* qh = q + (size_t)hq * D;
-    const float q0 = qh[i], q1 = qh[i + HALF];
-    s_q[i] = q0 * cs[i] - q1 * sn[i];
-    s_q[i + HALF] = q0 * sn[i] + q1 * cs[i];
-    const float* kh = k + (size_t)kvh * D;
-    const float k0 = kh[i], k1 = kh[i + HALF];
-    s_knew[i] = f32_to_bf16_bits(k0 * cs[i] - k1 * sn[i]);
-    s_knew[i + HALF] = f32_to_bf16_bits(k0 * sn[i] + k1 * cs[i]);
+  if (tid < HALF) {
+    const float c = rope_cos[(size_t)pos * HALF + tid], sn = rope_sin[(size_t)pos * HALF + tid];
+    s_q[tid] = q0 * c - q1 * sn;
+    s_q[tid + HALF] = q0 * sn + q1 * c;
+    s_knew[tid] = f32_to_bf16_bits(k0 * c - k1 * sn);
+    s_knew[tid + HALF] = f32_to_bf16_bits(k0 * sn + k1 * c);
+    s_vnew[tid] = f32_to_bf16_bits(v0);
+    s_vnew[tid + HALF] = f32_to_bf16_bits(v1);
   }
-  for (int i = tid; i < D; i += 1024) s_vnew[i] = f32_to_bf16_bits(v[(size_t)kvh * D + i]);
   lds_barrier();
   if (hq % G == 0)
     for (int i = tid; i < D; i += 1024) {
