@@ -80,6 +80,12 @@ void nve_qkv_matvec_w4a16(const uint16_t *x, const uint8_t *q_nib, const float *
                           const float *v_awq, int Nv, uint16_t *q_out, uint16_t *k_out,
                           uint16_t *v_out, int K, void *stream);
 
+/* Replaces nve_dequant_w4a16 (cuda/nve_kernels.cu:397-433; the prefill path's weight
+ * expansion before a dense matmul).  out fp16 [N, K] = f16_rne(f32(nib - 8) * scale
+ * [* awq[k]]); awq may be NULL.  out 16-byte aligned. */
+void nve_dequant_w4a16(const uint8_t *nibbles, const float *scales, const float *awq, uint16_t *out,
+                       int N, int K, void *stream);
+
 /* =========================================================================
  * Status-returning entry points (dtype-generic twins of the launchers above).
  * ========================================================================= */
@@ -172,6 +178,21 @@ int nve_hip_q4_quantize(const void *w, int w_dtype, int N, int K, uint8_t *nibbl
  * aligned. */
 int nve_hip_q4_repack(const uint8_t *q4_blocks, int N, int K, uint8_t *nibbles,
                       float *scales, void *stream);
+
+/* Twin of nve_dequant_w4a16 with the output dtype F16, BF16 or F32 (F32 = the value
+ * before rounding; bit-identical to QuantizedTensor::to_f32_vec, src/quantize.rs:396-426,
+ * applied to the same weights). */
+int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float *awq, void *out,
+                       int out_dtype, int N, int K, void *stream);
+
+/* Prefill product Y[M, N] = X[M, K] * W[N, K]^T for int4 weights (the reference's
+ * GpuWeight::matmul_x for seq > 1, src/gpu_layer.rs:219-237: nve_dequant_w4a16 to fp16
+ * then a dense GEMM) in one kernel: each weight is rounded exactly as the dequant
+ * rounds it (to x's dtype: F16 as the reference, or BF16) and the products accumulate
+ * in fp32 on MFMA.  x [M, K] row-major F16/BF16 (16-byte aligned); awq [K] or NULL;
+ * out [M, N] row-major F16, BF16 or F32.  K % 64 == 0. */
+int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,
+                       const float *awq, void *out, int out_dtype, int N, int K, void *stream);
 
 /* ---- per-layer precision dispatch (src/gpu_layer.rs:1013-1025) -------------- */
 /* Returns 1 (W4A8) when NVE_NO_W4A8 is unset and layer_importance < threshold,

@@ -49,6 +49,10 @@ hipError_t launch_q8_rows(const void* x, int xdt, int M, int K, int8_t* xq, uint
                           hipStream_t stream);
 hipError_t launch_q4_quantize(const void* w, int wdt, size_t nblocks, uint8_t* nib, float* scales,
                               hipStream_t stream);
+hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, const float* awq,
+                             void* out, int out_dt, int N, int K, hipStream_t s);
+hipError_t launch_dequant_w4(const uint8_t* nib, const float* scales, const float* awq, void* out, int out_dt,
+                             int N, int K, hipStream_t stream);
 hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, float* scales,
                             hipStream_t stream);
 hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream);
@@ -242,6 +246,29 @@ int nve_hip_q4_repack(const uint8_t* q4_blocks, int N, int K, uint8_t* nibbles, 
   return from_hip(launch_q4_repack(q4_blocks, (size_t)N * (K / 32), nibbles, scales, (hipStream_t)stream));
 }
 
+int nve_hip_dequant_w4(const uint8_t* nibbles, const float* scales, const float* awq, void* out, int out_dtype,
+                       int N, int K, void* stream) {
+  if (!nibbles || !scales || !out) return set_status(NVE_ERR_NULL);
+  if (out_dtype != NVE_DT_F16 && out_dtype != NVE_DT_BF16 && out_dtype != NVE_DT_F32) return set_status(NVE_ERR_DTYPE);
+  if (N < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(nibbles, 16) || !aligned(scales, 4) || !aligned(out, 16) || (awq && !aligned(awq, 16)))
+    return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_dequant_w4(nibbles, scales, awq, out, out_dtype, N, K, (hipStream_t)stream));
+}
+
+int nve_hip_gemm_w4a16(const void* x, int x_dtype, int M, const uint8_t* nibbles, const float* scales,
+                       const float* awq, void* out, int out_dtype, int N, int K, void* stream) {
+  if (!x || !nibbles || !scales || !out) return set_status(NVE_ERR_NULL);
+  if (x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) return set_status(NVE_ERR_DTYPE);
+  if (out_dtype != NVE_DT_F16 && out_dtype != NVE_DT_BF16 && out_dtype != NVE_DT_F32) return set_status(NVE_ERR_DTYPE);
+  if (M < 1 || N < 1 || K < 64 || K % 64 != 0) return set_status(NVE_ERR_SHAPE);
+  if (K > NVE_MAX_K) return set_status(NVE_ERR_TOO_LARGE);
+  if (!aligned(x, 16) || !aligned(nibbles, 16) || !aligned(scales, 4) || (awq && !aligned(awq, 16)) ||
+      !aligned(out, out_dtype == NVE_DT_F32 ? 4 : 2))
+    return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_gemm_w4a16(x, x_dtype, M, nibbles, scales, awq, out, out_dtype, N, K, (hipStream_t)stream));
+}
+
 // ---- dispatch -------------------------------------------------------------------------
 // src/gpu_layer.rs:1013-1025: NVE_NO_W4A8 set (any value) -> W4A16; otherwise W4A8
 // when importance < NVE_W4A8_THRESHOLD, a double parsed like Rust's str::parse::<f64>
@@ -352,6 +379,11 @@ void nve_matvec_w4a16(const uint16_t* x, const uint8_t* nibbles, const float* sc
                       const float* awq, uint16_t* out, int N, int K, void* stream) {
   report("nve_matvec_w4a16",
          nve_hip_matvec_w4a16(x, NVE_DT_F16, nibbles, scales, awq, out, NVE_DT_F16, N, K, stream));
+}
+
+void nve_dequant_w4a16(const uint8_t* nibbles, const float* scales, const float* awq, uint16_t* out, int N, int K,
+                       void* stream) {
+  report("nve_dequant_w4a16", nve_hip_dequant_w4(nibbles, scales, awq, out, NVE_DT_F16, N, K, stream));
 }
 
 void nve_qkv_matvec_w4a16(const uint16_t* x, const uint8_t* q_nib, const float* q_sc,

@@ -158,9 +158,16 @@ __device__ __forceinline__ float load_act<NVE_DT_F32>(const void* p, size_t i) {
 
 template <int DT>
 __device__ __forceinline__ void store_out(void* p, size_t i, float v);
+// f32 -> f16, round to nearest even, of a value that is first materialised as f32:
+// without the barrier the compiler may fuse the producing multiply with the
+// conversion (v_fma_mix), rounding the exact product once instead of twice.
+__device__ __forceinline__ _Float16 f32_to_f16_rne(float v) {
+  asm volatile("" : "+v"(v));
+  return (_Float16)v;
+}
 template <>
 __device__ __forceinline__ void store_out<NVE_DT_F16>(void* p, size_t i, float v) {
-  ((_Float16*)p)[i] = (_Float16)v;  // round to nearest even
+  ((_Float16*)p)[i] = f32_to_f16_rne(v);
 }
 template <>
 __device__ __forceinline__ void store_out<NVE_DT_BF16>(void* p, size_t i, float v) {

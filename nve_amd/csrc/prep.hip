@@ -191,9 +191,84 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
   if (a == 0x12345678u) sink[blockIdx.x & 1023] = 1.0f;
 }
 
+// ---- W4 dequantization (prefill path) ---------------------------------------
+// _nve_dequant_w4a16 (cuda/nve_kernels.cu:397-433): w[n, k] = f32(nibble - 8) * scale,
+// times awq[k] when given (a second f32 rounding, as QuantizedTensor::to_f32_vec does
+// it, src/quantize.rs:396-426), then rounded to the output type (RNE).  One thread per
+// 32-weight block: one 16-byte nibble load, 32 outputs written as 64/128 contiguous
+// bytes.
+template <int OUT_DT>
+__global__ __launch_bounds__(256) void dequant_w4_kernel(const uint8_t* __restrict__ nib,
+                                                         const float* __restrict__ scales,
+                                                         const float* __restrict__ awq, void* __restrict__ out,
+                                                         size_t nblocks, int nb) {
+  const size_t blk = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= nblocks) return;
+  const uint4 w = ((const uint4*)nib)[blk];
+  const float s = scales[blk];
+  const int col0 = (int)(blk % (size_t)nb) * 32;
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+  float v[32];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t byte = (d[t] >> (8 * e)) & 0xffu;
+      v[4 * t + e] = (float)((int)(byte & 15u) - 8) * s;       // element 4t+e
+      v[16 + 4 * t + e] = (float)((int)(byte >> 4) - 8) * s;   // element 16+4t+e
+    }
+  if (awq) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 a = ((const float4*)(awq + col0))[i];
+      v[4 * i] *= a.x;
+      v[4 * i + 1] *= a.y;
+      v[4 * i + 2] *= a.z;
+      v[4 * i + 3] *= a.w;
+    }
+  }
+  if (OUT_DT == NVE_DT_F32) {
+    float4* o = (float4*)((float*)out + blk * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  } else {
+    uint4* o = (uint4*)((uint16_t*)out + blk * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t q[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float a = v[8 * i + 2 * t], b = v[8 * i + 2 * t + 1];
+        if (OUT_DT == NVE_DT_BF16)
+          q[t] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+        else
+          q[t] = (uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(a)) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(b)) << 16);
+      }
+      o[i] = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
+}
+
 }  // namespace nve
 
 namespace nve_host {
+
+hipError_t launch_dequant_w4(const uint8_t* nib, const float* scales, const float* awq, void* out, int out_dt,
+                             int N, int K, hipStream_t stream) {
+  const size_t nblocks = (size_t)N * (K / 32);
+  const unsigned grid = (unsigned)((nblocks + 255) / 256);
+  if (out_dt == NVE_DT_F32)
+    hipLaunchKernelGGL(nve::dequant_w4_kernel<NVE_DT_F32>, dim3(grid), dim3(256), 0, stream, nib, scales, awq, out,
+                       nblocks, K / 32);
+  else if (out_dt == NVE_DT_BF16)
+    hipLaunchKernelGGL(nve::dequant_w4_kernel<NVE_DT_BF16>, dim3(grid), dim3(256), 0, stream, nib, scales, awq, out,
+                       nblocks, K / 32);
+  else
+    hipLaunchKernelGGL(nve::dequant_w4_kernel<NVE_DT_F16>, dim3(grid), dim3(256), 0, stream, nib, scales, awq, out,
+                       nblocks, K / 32);
+  return hipGetLastError();
+}
 
 hipError_t launch_q8_group(const void* x, int xdt, size_t total, int8_t* xq, float* scales,
                            hipStream_t stream) {

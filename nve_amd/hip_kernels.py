@@ -203,6 +203,31 @@ def q4_repack(q4_blocks: torch.Tensor, n: int, k: int) -> tuple[torch.Tensor, to
     return nib, sc
 
 
+def dequant_w4(nibbles: torch.Tensor, scales: torch.Tensor, n: int, k: int, awq: torch.Tensor | None = None,
+               dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """nve_dequant_w4a16 (cuda/nve_kernels.cu:397-433), the prefill path's weight expansion:
+    W [N, K] = (nibble - 8) * scale [* awq], in fp16 (the reference), bf16 or fp32."""
+    out = torch.empty((n, k), dtype=dtype, device=nibbles.device)
+    check("nve_hip_dequant_w4",
+          lib().nve_hip_dequant_w4(_dev(nibbles, "nibbles"), _dev(scales, "scales"),
+                                   None if awq is None else _dev(awq, "awq"), out.data_ptr(), _dt(out), n, k,
+                                   _stream()))
+    return out
+
+
+def gemm_w4a16(x: torch.Tensor, nibbles: torch.Tensor, scales: torch.Tensor, n: int, k: int,
+               awq: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Prefill x [M, K] @ W^T for int4 W: GpuWeight::matmul_x with seq > 1
+    (src/gpu_layer.rs:219-237, dequant to fp16 then matmul) fused into one MFMA kernel."""
+    m = x.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    check("nve_hip_gemm_w4a16",
+          lib().nve_hip_gemm_w4a16(_dev(x, "x"), _dt(x), m, _dev(nibbles, "nibbles"), _dev(scales, "scales"),
+                                   None if awq is None else _dev(awq, "awq"), out.data_ptr(), _dt(out), n, k,
+                                   _stream()))
+    return out
+
+
 def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
     """HBM streaming probe (reads every byte of buf once)."""
     check("nve_hip_stream_read",

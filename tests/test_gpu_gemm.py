@@ -1,0 +1,98 @@
+"""GPU parity of the W4A16 prefill GEMM (nve_hip_gemm_w4a16) and of the weight
+dequantization it fuses.
+
+Reference semantics (GpuWeight::matmul_x for seq > 1, src/gpu_layer.rs:219-237): the
+int4 weights are expanded with nve_dequant_w4a16 (f32 (nibble - 8) * scale [* awq],
+rounded to fp16) and multiplied by the fp16 activations in a dense GEMM.  The oracle
+forms the same rounded weights from QuantizedTensor::to_f32_vec (restated in
+oracle/oracle.c) and multiplies in float64; the kernel accumulates in fp32 on MFMA.
+Bars: the weights the GEMM multiplies are bit-identical to the reference's dequant
+(checked exactly with an identity activation matrix); products: the W4A16 bar,
+rel = max_i |y_i - ref_i| / max(|ref_i|, 1e-3 rms(ref)) <= 2e-3 for fp32 output
+(fp32 accumulation over K terms in MFMA order; measured ~1e-3 at the near-zero floor
+for K = 8192), plus 2^-8 (bf16) / 2^-11 (fp16) for rounded outputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import rel_err_floor, to_bf16, weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+@pytest.fixture(scope="module")
+def hk(torch_dev):
+    from nve_amd import hip_kernels
+    return hip_kernels
+
+
+def _round(a, dt):
+    return a.astype(np.float16).astype(np.float32) if dt == "f16" else to_bf16(a)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("with_awq", [False, True])
+def test_gemm_w4a16_parity(orc, torch_dev, hk, m, n, k, xdt, with_awq):
+    torch = torch_dev
+    print(f"gemm m={m} n={n} k={k} x={xdt} awq={with_awq}", flush=True)
+    rng = np.random.default_rng(m * 7 + n + k)
+    data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.05))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    awq = rng.uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
+    wref = _round(orc.q4_to_f32(data, n, k, awq), xdt).astype(np.float64)
+    x = _round(rng.standard_normal((m, k)).astype(np.float32), xdt)
+    ref = x.astype(np.float64) @ wref.T
+    tdt = torch.float16 if xdt == "f16" else torch.bfloat16
+    xt = torch.from_numpy(x).cuda().to(tdt)
+    y = hk.gemm_w4a16(xt, torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda(), n, k,
+                      None if awq is None else torch.from_numpy(awq).cuda(), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err_floor(y.cpu().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("with_awq", [False, True])
+def test_gemm_w4a16_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_awq):
+    """X = I: every output is one product 1 * w (exact in fp32), so Y^T is the weight
+    matrix as the GEMM rounded it, which must equal the reference dequant bit for bit
+    (including halfway cases, where a fused multiply-convert would round differently)."""
+    torch = torch_dev
+    n, k = 130, 512
+    data = orc.q4_from_f32(weights(n, k, seed=31, std=0.3))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    awq = np.random.default_rng(32).uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
+    wref = _round(orc.q4_to_f32(data, n, k, awq), xdt)
+    tdt = torch.float16 if xdt == "f16" else torch.bfloat16
+    eye = torch.eye(k, dtype=tdt, device="cuda")
+    y = hk.gemm_w4a16(eye, torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda(), n, k,
+                      None if awq is None else torch.from_numpy(awq).cuda(), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().T.view(np.uint32), wref.view(np.uint32))
+
+
+@pytest.mark.parametrize("odt,tol", [("bf16", 2.0 ** -8 + 2e-3), ("f16", 2.0 ** -11 + 2e-3)])
+def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol):
+    torch = torch_dev
+    m, n, k = 33, 192, 2048
+    rng = np.random.default_rng(5)
+    data = orc.q4_from_f32(weights(n, k, seed=9, std=0.05))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    wref = orc.q4_to_f32(data, n, k).astype(np.float16).astype(np.float64)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    ref = x.astype(np.float64) @ wref.T
+    out_dt = torch.bfloat16 if odt == "bf16" else torch.float16
+    y = hk.gemm_w4a16(torch.from_numpy(x).cuda(), torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda(), n, k,
+                      out_dtype=out_dt)
+    torch.cuda.synchronize()
+    assert rel_err_floor(y.float().cpu().numpy(), ref) <= tol

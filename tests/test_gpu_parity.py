@@ -283,6 +283,45 @@ def test_q4_repack_device_bit_exact(orc, torch_dev, hk):
     assert np.array_equal(down(nib), nib_ref) and np.array_equal(down(sc), sc_ref)
 
 
+@pytest.mark.parametrize("with_awq", [False, True])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_dequant_w4_bit_exact(orc, torch_dev, hk, dtype, with_awq):
+    """nve_dequant_w4a16 / nve_hip_dequant_w4 against QuantizedTensor::to_f32_vec
+    (restated as orc.q4_to_f32) on the same weights, then rounded like the kernel."""
+    torch = torch_dev
+    n, k = 67, 2048
+    w = weights(n, k, seed=21, std=0.5)
+    data = orc.q4_from_f32(w)
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    awq = (np.random.default_rng(22).uniform(0.25, 4.0, k).astype(np.float32)) if with_awq else None
+    ref = orc.q4_to_f32(data, n, k, awq)
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    out = hk.dequant_w4(up(torch, nib), up(torch, sc), n, k, None if awq is None else up(torch, awq), dtype=tdt)
+    torch.cuda.synchronize()
+    if dtype == "f32":
+        assert np.array_equal(down(out).view(np.uint32), ref.view(np.uint32))
+    elif dtype == "f16":
+        assert np.array_equal(down(out).view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    else:
+        got = down(out.view(torch.int16)).view(np.uint16)
+        assert np.array_equal(got, orc.f32_to_bf16_bits(ref).reshape(ref.shape))
+
+
+def test_dequant_w4a16_drop_in(orc, torch_dev, hk):
+    from nve_amd._lib import lib
+    torch = torch_dev
+    n, k = 40, 4096
+    data = orc.q4_from_f32(weights(n, k, seed=23))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    out = torch.empty((n, k), dtype=torch.float16, device="cuda")
+    tn, ts = up(torch, nib), up(torch, sc)
+    lib().nve_dequant_w4a16(tn.data_ptr(), ts.data_ptr(), None, out.data_ptr(), n, k,
+                            torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert lib().nve_hip_last_status() == 0
+    assert np.array_equal(down(out).view(np.uint16), orc.q4_to_f32(data, n, k).astype(np.float16).view(np.uint16))
+
+
 # ---------------------------------------------------------------------------
 # batched W4A8
 # ---------------------------------------------------------------------------
