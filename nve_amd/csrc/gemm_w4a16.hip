@@ -10,10 +10,10 @@
 // the tile product runs on v_mfma_f32_16x16x32_{f16,bf16} with fp32 accumulation.
 // Weight traffic: 0.625 B per weight instead of 0.625 + 2 (write) + 2 (read).
 //
-// Tiling: 128 x 128 output tile per workgroup of 4 waves (2 x 2), 64 x 64 per wave as
-// 4 x 4 MFMA tiles of 16 x 16; K advances 64 per slice (two Q4 blocks).  The global
-// loads (X rows, nibbles, scales) of the next two slices are in flight in a pair of
-// register stages while a slice is staged and multiplied, so HBM latency overlaps the
+// Tiling: 128 x 128 output tile per workgroup of 8 waves (4 x 2), 32 x 64 per wave as
+// 2 x 4 MFMA tiles of 16 x 16; K advances 64 per slice (two Q4 blocks).  The global
+// loads (X rows, nibbles, scales) of the next slice are in flight while a slice is
+// staged and multiplied, so HBM latency overlaps the
 // math; small-M launches also split K over workgroups (fp32 atomic accumulation).  LDS rows are padded
 // (72 elements) so the ds_read_b128 of a fragment spreads over the banks.
 //
@@ -45,144 +45,144 @@ __device__ __forceinline__ f4_t mfma16(uint4 a, uint4 b, f4_t c) {
 
 template <bool AWQ>
 struct GemmStage {
-  uint4 rx0, rx1, rx2, rx3;  // four 16-byte pieces of the X slice (scalars: kept in VGPRs)
-  uint4 rn;
+  uint4 rx0, rx1;  // two 16-byte pieces of the X slice (rows r and r + 64)
+  uint2 rn;        // half a Q4 block: bytes 8h .. 8h+7 (elements 8h..8h+7 and 16+8h..16+8h+7)
   float rs;
-  float4 ra[AWQ ? 8 : 1];
+  float4 ra[AWQ ? 4 : 1];
 };
 
+// Thread t of the 512: X pieces (row t/8 and t/8 + 64, columns 8 (t%8) .. +7); weight
+// half-block h = t & 1 of block t/2 (tile row t/4, block (t/2) & 1 of the slice).
 template <bool AWQ>
 __device__ __forceinline__ void gemm_issue(GemmStage<AWQ>& st, const uint16_t* __restrict__ x,
                                            const uint8_t* __restrict__ nib, const float* __restrict__ scales,
                                            const float* __restrict__ awq, int tid, int m0, int M, int K, int wn_g,
                                            int wblk, int k0) {
-  const int r = tid >> 3, c8 = tid & 7;  // piece i covers row r + 32 i, columns 8 c8 .. + 7
+  const int r = tid >> 3, c8 = tid & 7;
   const uint16_t* xp = x + (size_t)k0 + 8 * c8;
   st.rx0 = *(const uint4*)(xp + (size_t)min(m0 + r, M - 1) * K);
-  st.rx1 = *(const uint4*)(xp + (size_t)min(m0 + r + 32, M - 1) * K);
-  st.rx2 = *(const uint4*)(xp + (size_t)min(m0 + r + 64, M - 1) * K);
-  st.rx3 = *(const uint4*)(xp + (size_t)min(m0 + r + 96, M - 1) * K);
-  const int b = (k0 >> 5) + wblk;
-  st.rn = ld_stream((const uint4*)(nib + (size_t)wn_g * (K >> 1)) + b);
+  st.rx1 = *(const uint4*)(xp + (size_t)min(m0 + r + 64, M - 1) * K);
+  const int b = (k0 >> 5) + wblk, h = tid & 1;
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 nv = __builtin_nontemporal_load((const u32x2*)(nib + (size_t)wn_g * (K >> 1) + 16 * b + 8 * h));
+  st.rn = make_uint2(nv.x, nv.y);
   st.rs = scales[(size_t)wn_g * (K >> 5) + b];
   if (AWQ) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) st.ra[i] = ((const float4*)(awq + 32 * b))[i];
+    const float4* ap = (const float4*)(awq + 32 * b + 8 * h);
+    st.ra[0] = ap[0];
+    st.ra[1] = ap[1];
+    st.ra[2] = ap[4];  // elements 16 + 8h ..
+    st.ra[3] = ap[5];
   }
 }
 
-// X slice to LDS; the weight block dequantized (element j = low nibble of byte j,
-// element j + 16 = high nibble) and rounded to the activation type into LDS.
+// X slice to LDS; the half block dequantized and rounded to the activation type into
+// LDS: elements 8h .. 8h+7 (low nibbles of its bytes) and 16+8h .. 16+8h+7 (high).
 template <bool BF16, bool AWQ>
 __device__ __forceinline__ void gemm_stage(const GemmStage<AWQ>& st, uint16_t* sX, uint16_t* sW, int tid, int wrow,
                                            int wblk) {
   const int r = tid >> 3, c8 = tid & 7;
   uint16_t* xd = sX + r * GM_LD + 8 * c8;
   *(uint4*)(xd) = st.rx0;
-  *(uint4*)(xd + 32 * GM_LD) = st.rx1;
-  *(uint4*)(xd + 64 * GM_LD) = st.rx2;
-  *(uint4*)(xd + 96 * GM_LD) = st.rx3;
-  const uint32_t d[4] = {st.rn.x, st.rn.y, st.rn.z, st.rn.w};
-  float v[32];
+  *(uint4*)(xd + 64 * GM_LD) = st.rx1;
+  const int h = tid & 1;
+  const uint32_t d[2] = {st.rn.x, st.rn.y};
+  float lo[8], hi[8];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t byte = (d[t] >> (8 * e)) & 0xffu;
-      v[4 * t + e] = (float)((int)(byte & 15u) - 8) * st.rs;
-      v[16 + 4 * t + e] = (float)((int)(byte >> 4) - 8) * st.rs;
+      lo[4 * t + e] = (float)((int)(byte & 15u) - 8) * st.rs;
+      hi[4 * t + e] = (float)((int)(byte >> 4) - 8) * st.rs;
     }
   if (AWQ) {
+    const float a[16] = {st.ra[0].x, st.ra[0].y, st.ra[0].z, st.ra[0].w, st.ra[1].x, st.ra[1].y, st.ra[1].z, st.ra[1].w,
+                         st.ra[2].x, st.ra[2].y, st.ra[2].z, st.ra[2].w, st.ra[3].x, st.ra[3].y, st.ra[3].z, st.ra[3].w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      v[4 * i] *= st.ra[i].x;
-      v[4 * i + 1] *= st.ra[i].y;
-      v[4 * i + 2] *= st.ra[i].z;
-      v[4 * i + 3] *= st.ra[i].w;
+      lo[i] *= a[i];
+      hi[i] *= a[8 + i];
     }
   }
+  uint16_t* dst = sW + wrow * GM_LD + 32 * wblk + 8 * h;
   // (pack2 rounds each product as an f32 value first: two roundings, as the
   // reference's dequant does them)
-  uint16_t* dst = sW + wrow * GM_LD + 32 * wblk;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *(uint4*)(dst + 8 * q) = make_uint4(pack2<BF16>(v[8 * q], v[8 * q + 1]), pack2<BF16>(v[8 * q + 2], v[8 * q + 3]),
-                                        pack2<BF16>(v[8 * q + 4], v[8 * q + 5]), pack2<BF16>(v[8 * q + 6], v[8 * q + 7]));
+  *(uint4*)(dst) = make_uint4(pack2<BF16>(lo[0], lo[1]), pack2<BF16>(lo[2], lo[3]), pack2<BF16>(lo[4], lo[5]),
+                              pack2<BF16>(lo[6], lo[7]));
+  *(uint4*)(dst + 16) = make_uint4(pack2<BF16>(hi[0], hi[1]), pack2<BF16>(hi[2], hi[3]), pack2<BF16>(hi[4], hi[5]),
+                                   pack2<BF16>(hi[6], hi[7]));
 }
 
-// One K slice: stage it in LDS, then the wave's 4 x 4 MFMA tiles over its 64 columns.
-template <bool BF16, bool AWQ>
-__device__ __forceinline__ void gemm_slice(const GemmStage<AWQ>& st, uint16_t* sX, uint16_t* sW, int tid, int wrow,
-                                           int wblk, int wm, int wn, int lane, f4_t (&acc)[4][4]) {
-  gemm_stage<BF16, AWQ>(st, sX, sW, tid, wrow, wblk);
-  lds_barrier();
+// The wave's 2 x 4 MFMA tiles (32 rows x 64 columns) over one staged K slice.
+template <bool BF16>
+__device__ __forceinline__ void gemm_mfma(const uint16_t* sX, const uint16_t* sW, int wm, int wn, int lane,
+                                          f4_t (&acc)[2][4]) {
   const int fr = lane & 15, fk = 8 * (lane >> 4);
 #pragma unroll
   for (int kk = 0; kk < GM_BK; kk += 32) {
-    uint4 a[4], b[4];
+    uint4 a[2], b[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *(const uint4*)(sX + (64 * wm + 16 * i + fr) * GM_LD + kk + fk);
+    for (int i = 0; i < 2; ++i) a[i] = *(const uint4*)(sX + (32 * wm + 16 * i + fr) * GM_LD + kk + fk);
 #pragma unroll
     for (int j = 0; j < 4; ++j) b[j] = *(const uint4*)(sW + (64 * wn + 16 * j + fr) * GM_LD + kk + fk);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<BF16>(a[i], b[j], acc[i][j]);
   }
-  lds_barrier();  // the tile is rewritten by the next slice
 }
 
 // SPLIT: the K range is divided over gridDim.z workgroups per output tile, which add
 // their fp32 partial sums into a zeroed fp32 output (launches whose tile grid alone
 // would leave most CUs idle: small M).
 template <bool BF16, bool AWQ, int OUT_DT, bool SPLIT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_w4a16_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ nib, const float* __restrict__ scales,
-    const float* __restrict__ awq, void* __restrict__ out, int M, int N, int K, int k_split) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 4))) void gemm_w4a16_kernel(const uint16_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ nib,
+                                                         const float* __restrict__ scales,
+                                                         const float* __restrict__ awq, void* __restrict__ out,
+                                                         int M, int N, int K, int k_split) {
   __shared__ __align__(16) uint16_t sX[GM_BM * GM_LD];
   __shared__ __align__(16) uint16_t sW[GM_BN * GM_LD];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves: 32 rows x 64 columns each
   const int m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
-  const int nb = K >> 5;
 
-  // global -> register staging of one K slice: 4 x 16 B of X and one Q4 block per thread
   GemmStage<AWQ> st;
-  const int wrow = tid >> 1, wblk = tid & 1;  // weight row in the tile, block within the slice
+  const int wrow = tid >> 2, wblk = (tid >> 1) & 1;  // weight row in the tile, block within the slice
   const int wn_g = min(n0 + wrow, N - 1);
 
-  f4_t acc[4][4];
+  f4_t acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int fr = lane & 15;
   const int kb = SPLIT ? blockIdx.z * k_split : 0;
   const int ke = SPLIT ? min(K, kb + k_split) : K;
-  // two slices in flight: a pair of register stages, issued unconditionally (slice
-  // indices past the range re-read the last slice) so no wait covers a younger stage
-  const int klast = ke - GM_BK;
-  GemmStage<AWQ> s1;
+  // the next slice is in flight while a slice is staged and multiplied; the issue is
+  // unconditional (the last slice re-reads itself), which keeps the staging registers
+  // out of a conditional merge
   gemm_issue<AWQ>(st, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, kb);
-  gemm_issue<AWQ>(s1, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, min(kb + GM_BK, klast));
-  for (int k0 = kb; k0 < ke; k0 += 2 * GM_BK) {
-    gemm_slice<BF16, AWQ>(st, sX, sW, tid, wrow, wblk, wm, wn, lane, acc);
-    gemm_issue<AWQ>(st, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, min(k0 + 2 * GM_BK, klast));
-    if (k0 + GM_BK < ke) gemm_slice<BF16, AWQ>(s1, sX, sW, tid, wrow, wblk, wm, wn, lane, acc);
-    gemm_issue<AWQ>(s1, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, min(k0 + 3 * GM_BK, klast));
+  for (int k0 = kb; k0 < ke; k0 += GM_BK) {
+    gemm_stage<BF16, AWQ>(st, sX, sW, tid, wrow, wblk);
+    lds_barrier();
+    gemm_issue<AWQ>(st, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, min(k0 + GM_BK, ke - GM_BK));
+    gemm_mfma<BF16>(sX, sW, wm, wn, lane, acc);
+    lds_barrier();  // the tile is rewritten by the next slice
   }
 
   // D[4(l/16) + e][l%16] of tile (i, j)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + 64 * wn + 16 * j + fr;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + e;
+        const int m = m0 + 32 * wm + 16 * i + 4 * (lane >> 4) + e;
         if (m < M && n < N) {
           if (SPLIT)
             atomicAdd((float*)out + (size_t)m * N + n, acc[i][j][e]);
@@ -223,7 +223,7 @@ static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const 
   const int k_split = ((kit + split - 1) / split) * nve::GM_BK;
   const dim3 grid(tn, tm, split);
 #define NVE_GEMM(OD, SP)                                                                                       \
-  hipLaunchKernelGGL((nve::gemm_w4a16_kernel<BF16, AWQ, OD, SP>), grid, dim3(256), 0, s, (const uint16_t*)x, nib, \
+  hipLaunchKernelGGL((nve::gemm_w4a16_kernel<BF16, AWQ, OD, SP>), grid, dim3(512), 0, s, (const uint16_t*)x, nib, \
                      sc, awq, out, M, N, K, k_split)
   if (split > 1) {
     NVE_GEMM(NVE_DT_F32, true);
