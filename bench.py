@@ -42,6 +42,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "W4A8/W4A16 GEMV GB/s & % HBM peak at 8B shapes; decode tok/s (1 GPU)"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16
 
 SUITE_8B = [  # name, N, K
     ("q_proj", 4096, 4096),
@@ -447,6 +448,48 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool) -> d
     return rec
 
 
+def prefill_gemm(torch, hk, reps: int = 20) -> dict:
+    """The prefill-adjacency row: W4A16 GEMM X[M, K] @ W^T at the 8B gate shape
+    (14336 x 4096), fp16 activations, fp32 output, M in {16, 128, 512, 2048}: the fused
+    MFMA kernel (nve_hip_gemm_w4a16) against the reference's own method on the same GPU
+    (nve_dequant_w4a16 to fp16, then a dense fp16 GEMM -- torch.matmul, i.e. the
+    vendor BLAS -- as GpuWeight::matmul_x does with candle, src/gpu_layer.rs:219-237).
+    Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time."""
+    g = torch.Generator(device="cuda").manual_seed(17)
+    n, k = 14336, 4096
+    nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
+    out = {"shape": f"{n}x{k}", "x_dtype": "f16", "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS, "rows": []}
+    for m in (16, 128, 512, 2048):
+        x = torch.randn((m, k), generator=g, device="cuda").half()
+        wf = hk.dequant_w4(nib, sc, n, k)
+
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for _ in range(reps):
+                    fn()
+            gr.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / reps
+
+        us = timed(lambda: hk.gemm_w4a16(x, nib, sc, n, k))
+        us_ref = timed(lambda: hk.dequant_w4(nib, sc, n, k)) + timed(lambda: torch.matmul(x, wf.t()))
+        fl = 2.0 * m * n * k
+        out["rows"].append({"M": m, "fused_us": round(us, 1), "fused_TFLOPs": round(fl / us / 1e6, 1),
+                            "frac_mfma_peak": round(fl / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
+                            "dequant_plus_blas_us": round(us_ref, 1)})
+        log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us")
+        del x, wf
+    return out
+
+
 def traffic_probe(torch, L, hk):
     """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
     256 MiB (calibration: 256 MiB read + 256 MiB written), then 5 launches of the
@@ -552,6 +595,8 @@ def main():
     torch.cuda.empty_cache()
     decode = None if args.no_decode else decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens,
                                                    args.no_cpu)
+    log("prefill W4A16 GEMM:")
+    prefill = prefill_gemm(torch, hk)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     # HBM bytes per launch of the roofline kernel, from the calibrated rocprofv3
@@ -604,6 +649,7 @@ def main():
         "hbm_stream_probe_GBs": round(stream_gbs, 1),
         "batched_w4a8_8b": sweep,
         "decode_3b": decode,
+        "prefill_w4a16_gemm": prefill,
     }
     print(json.dumps(rec), flush=True)
 
