@@ -7,18 +7,17 @@
 // without the expanded matrix ever reaching HBM: each workgroup dequantizes its
 // 128 x 64 weight slice once into LDS, rounded exactly as the reference's dequant
 // rounds it (f32 (nibble - 8) * scale [* awq], then RNE to the activation type), and
-// the tile product runs on v_mfma_f32_16x16x32_{f16,bf16} with fp32 accumulation.
+// the tile product runs on v_mfma_f32_32x32x16_{f16,bf16} with fp32 accumulation.
 // Weight traffic: 0.625 B per weight instead of 0.625 + 2 (write) + 2 (read).
 //
-// Tiling: 128 x 128 output tile per workgroup of 8 waves (4 x 2), 32 x 64 per wave as
-// 2 x 4 MFMA tiles of 16 x 16; K advances 64 per slice (two Q4 blocks).  The global
-// loads (X rows, nibbles, scales) of the next slice are in flight while a slice is
-// staged and multiplied, so HBM latency overlaps the
+// Tiling: 128 x 128 output tile per workgroup of 4 waves (2 x 2), 64 x 64 per wave as
+// 2 x 2 MFMA tiles of 32 x 32 (v_mfma_f32_32x32x16: half the LDS operand traffic per
+// flop of 16 x 16 tiles); K advances 64 per slice (two Q4 blocks).  The global
+// loads (X rows, nibbles, scales) run two slices ahead of the MFMAs and the LDS is
+// double-buffered, so the dequantization of slice t+1 overlaps the MFMAs of slice t, so HBM latency overlaps the
 // math; small-M launches also split K over workgroups (fp32 atomic accumulation).  LDS rows are padded
 // (72 elements) so the ds_read_b128 of a fragment spreads over the banks.
-//
-// MFMA operand layout (16x16x32): lane l supplies A[l%16][8(l/16) .. +7] and
-// B[8(l/16) .. +7][l%16]; it receives D[4(l/16) .. +3][l%16].
+
 #include "common.h"
 #include "w4_launch.h"
 
@@ -43,93 +42,92 @@ __device__ __forceinline__ f4_t mfma16(uint4 a, uint4 b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
 }
 
-template <bool AWQ>
-struct GemmStage {
-  uint4 rx0, rx1;  // two 16-byte pieces of the X slice (rows r and r + 64)
-  uint2 rn;        // half a Q4 block: bytes 8h .. 8h+7 (elements 8h..8h+7 and 16+8h..16+8h+7)
-  float rs;
-  float4 ra[AWQ ? 4 : 1];
-};
+typedef float f16x_t __attribute__((ext_vector_type(16)));
 
-// Thread t of the 512: X pieces (row t/8 and t/8 + 64, columns 8 (t%8) .. +7); weight
-// half-block h = t & 1 of block t/2 (tile row t/4, block (t/2) & 1 of the slice).
-template <bool AWQ>
-__device__ __forceinline__ void gemm_issue(GemmStage<AWQ>& st, const uint16_t* __restrict__ x,
-                                           const uint8_t* __restrict__ nib, const float* __restrict__ scales,
-                                           const float* __restrict__ awq, int tid, int m0, int M, int K, int wn_g,
-                                           int wblk, int k0) {
-  const int r = tid >> 3, c8 = tid & 7;
-  const uint16_t* xp = x + (size_t)k0 + 8 * c8;
-  st.rx0 = *(const uint4*)(xp + (size_t)min(m0 + r, M - 1) * K);
-  st.rx1 = *(const uint4*)(xp + (size_t)min(m0 + r + 64, M - 1) * K);
-  const int b = (k0 >> 5) + wblk, h = tid & 1;
-  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 nv = __builtin_nontemporal_load((const u32x2*)(nib + (size_t)wn_g * (K >> 1) + 16 * b + 8 * h));
-  st.rn = make_uint2(nv.x, nv.y);
-  st.rs = scales[(size_t)wn_g * (K >> 5) + b];
-  if (AWQ) {
-    const float4* ap = (const float4*)(awq + 32 * b + 8 * h);
-    st.ra[0] = ap[0];
-    st.ra[1] = ap[1];
-    st.ra[2] = ap[4];  // elements 16 + 8h ..
-    st.ra[3] = ap[5];
-  }
+template <bool BF16>
+__device__ __forceinline__ f16x_t mfma32(uint4 a, uint4 b, f16x_t c) {
+  if (BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
 }
 
-// X slice to LDS; the half block dequantized and rounded to the activation type into
-// LDS: elements 8h .. 8h+7 (low nibbles of its bytes) and 16+8h .. 16+8h+7 (high).
-template <bool BF16, bool AWQ>
-__device__ __forceinline__ void gemm_stage(const GemmStage<AWQ>& st, uint16_t* sX, uint16_t* sW, int tid, int wrow,
-                                           int wblk) {
-  const int r = tid >> 3, c8 = tid & 7;
-  uint16_t* xd = sX + r * GM_LD + 8 * c8;
-  *(uint4*)(xd) = st.rx0;
-  *(uint4*)(xd + 64 * GM_LD) = st.rx1;
-  const int h = tid & 1;
-  const uint32_t d[2] = {st.rn.x, st.rn.y};
-  float lo[8], hi[8];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t byte = (d[t] >> (8 * e)) & 0xffu;
-      lo[4 * t + e] = (float)((int)(byte & 15u) - 8) * st.rs;
-      hi[4 * t + e] = (float)((int)(byte >> 4) - 8) * st.rs;
-    }
-  if (AWQ) {
-    const float a[16] = {st.ra[0].x, st.ra[0].y, st.ra[0].z, st.ra[0].w, st.ra[1].x, st.ra[1].y, st.ra[1].z, st.ra[1].w,
-                         st.ra[2].x, st.ra[2].y, st.ra[2].z, st.ra[2].w, st.ra[3].x, st.ra[3].y, st.ra[3].z, st.ra[3].w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      lo[i] *= a[i];
-      hi[i] *= a[8 + i];
-    }
-  }
-  uint16_t* dst = sW + wrow * GM_LD + 32 * wblk + 8 * h;
-  // (pack2 rounds each product as an f32 value first: two roundings, as the
-  // reference's dequant does them)
-  *(uint4*)(dst) = make_uint4(pack2<BF16>(lo[0], lo[1]), pack2<BF16>(lo[2], lo[3]), pack2<BF16>(lo[4], lo[5]),
-                              pack2<BF16>(lo[6], lo[7]));
-  *(uint4*)(dst + 16) = make_uint4(pack2<BF16>(hi[0], hi[1]), pack2<BF16>(hi[2], hi[3]), pack2<BF16>(hi[4], hi[5]),
-                                   pack2<BF16>(hi[6], hi[7]));
-}
+// Staging of one K slice, written as macros over the kernel's local registers (passing
+// a staging struct by reference to helper functions left it in scratch memory).
+// Thread t: X pieces (row t/8 + 32 i, columns 8 (t%8) .. +7); weight block t & 1 of
+// tile row t/2 (nontemporal: read once).
+#define GEMM_ISSUE(K0)                                                                          \
+  do {                                                                                          \
+    const uint16_t* xp_ = x + (size_t)(K0) + 8 * xc8;                                           \
+    rx0 = *(const uint4*)(xp_ + (size_t)min(m0 + xr, M - 1) * K);                               \
+    rx1 = *(const uint4*)(xp_ + (size_t)min(m0 + xr + 32, M - 1) * K);                          \
+    rx2 = *(const uint4*)(xp_ + (size_t)min(m0 + xr + 64, M - 1) * K);                          \
+    rx3 = *(const uint4*)(xp_ + (size_t)min(m0 + xr + 96, M - 1) * K);                          \
+    const int b_ = ((K0) >> 5) + wblk;                                                          \
+    rn = ld_stream((const uint4*)(nib + (size_t)wn_g * (K >> 1)) + b_);                         \
+    rs = scales[(size_t)wn_g * (K >> 5) + b_];                                                  \
+    if (AWQ) {                                                                                  \
+      _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) ra[i_] = ((const float4*)(awq + 32 * b_))[i_]; \
+    }                                                                                           \
+  } while (0)
 
-// The wave's 2 x 4 MFMA tiles (32 rows x 64 columns) over one staged K slice.
+// X pieces to LDS; the weight block dequantized and rounded to the activation type into
+// LDS.  (nibble - 8) * s is formed as fma(nibble, s, -8 s): -8 s is exact and n s - 8 s
+// is the exact product (n - 8) s, so the fma's single rounding equals the f32 product
+// the reference forms; byte extracts of the masked dword become v_cvt_f32_ubyte{0..3}
+// (element j = low nibble of byte j, element j + 16 = high nibble).  pack2 then rounds
+// each f32 value to the 16-bit type (two roundings, as the reference's dequant).
+#define GEMM_STAGE(DX, DW)                                                                      \
+  do {                                                                                          \
+    uint16_t* xd_ = (DX) + xr * GM_LD + 8 * xc8;                                                \
+    *(uint4*)(xd_) = rx0;                                                                       \
+    *(uint4*)(xd_ + 32 * GM_LD) = rx1;                                                          \
+    *(uint4*)(xd_ + 64 * GM_LD) = rx2;                                                          \
+    *(uint4*)(xd_ + 96 * GM_LD) = rx3;                                                          \
+    const uint32_t d_[4] = {rn.x, rn.y, rn.z, rn.w};                                            \
+    const float s8_ = -8.0f * rs;                                                               \
+    float v_[32];                                                                               \
+    _Pragma("unroll") for (int t_ = 0; t_ < 4; ++t_) {                                          \
+      const uint32_t lo_ = d_[t_] & 0x0F0F0F0Fu, hi_ = (d_[t_] >> 4) & 0x0F0F0F0Fu;             \
+      v_[4 * t_ + 0] = fmaf((float)(lo_ & 0xffu), rs, s8_);                                     \
+      v_[4 * t_ + 1] = fmaf((float)((lo_ >> 8) & 0xffu), rs, s8_);                              \
+      v_[4 * t_ + 2] = fmaf((float)((lo_ >> 16) & 0xffu), rs, s8_);                             \
+      v_[4 * t_ + 3] = fmaf((float)(lo_ >> 24), rs, s8_);                                       \
+      v_[16 + 4 * t_ + 0] = fmaf((float)(hi_ & 0xffu), rs, s8_);                                \
+      v_[16 + 4 * t_ + 1] = fmaf((float)((hi_ >> 8) & 0xffu), rs, s8_);                         \
+      v_[16 + 4 * t_ + 2] = fmaf((float)((hi_ >> 16) & 0xffu), rs, s8_);                        \
+      v_[16 + 4 * t_ + 3] = fmaf((float)(hi_ >> 24), rs, s8_);                                  \
+    }                                                                                           \
+    if (AWQ) {                                                                                  \
+      _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) {                                        \
+        v_[4 * i_] *= ra[i_].x;                                                                 \
+        v_[4 * i_ + 1] *= ra[i_].y;                                                             \
+        v_[4 * i_ + 2] *= ra[i_].z;                                                             \
+        v_[4 * i_ + 3] *= ra[i_].w;                                                             \
+      }                                                                                         \
+    }                                                                                           \
+    uint16_t* dst_ = (DW) + wrow * GM_LD + 32 * wblk;                                           \
+    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_)                                            \
+      *(uint4*)(dst_ + 8 * q_) =                                                                \
+          make_uint4(pack2<BF16>(v_[8 * q_], v_[8 * q_ + 1]), pack2<BF16>(v_[8 * q_ + 2], v_[8 * q_ + 3]), \
+                     pack2<BF16>(v_[8 * q_ + 4], v_[8 * q_ + 5]), pack2<BF16>(v_[8 * q_ + 6], v_[8 * q_ + 7])); \
+  } while (0)
+
+// The wave's 2 x 2 tiles of 32 x 32 (64 rows x 64 columns) over one staged K slice:
+// v_mfma_f32_32x32x16, lane l supplies A[l%32][8(l/32) .. +7] and B[8(l/32) .. +7][l%32].
 template <bool BF16>
 __device__ __forceinline__ void gemm_mfma(const uint16_t* sX, const uint16_t* sW, int wm, int wn, int lane,
-                                          f4_t (&acc)[2][4]) {
-  const int fr = lane & 15, fk = 8 * (lane >> 4);
+                                          f16x_t (&acc)[2][2]) {
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
 #pragma unroll
-  for (int kk = 0; kk < GM_BK; kk += 32) {
-    uint4 a[2], b[4];
+  for (int kk = 0; kk < GM_BK; kk += 16) {
+    uint4 a[2], b[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) a[i] = *(const uint4*)(sX + (32 * wm + 16 * i + fr) * GM_LD + kk + fk);
+    for (int i = 0; i < 2; ++i) a[i] = *(const uint4*)(sX + (64 * wm + 32 * i + fr) * GM_LD + kk + fk);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *(const uint4*)(sW + (64 * wn + 16 * j + fr) * GM_LD + kk + fk);
+    for (int j = 0; j < 2; ++j) b[j] = *(const uint4*)(sW + (64 * wn + 32 * j + fr) * GM_LD + kk + fk);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<BF16>(a[i], b[j], acc[i][j]);
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<BF16>(a[i], b[j], acc[i][j]);
   }
 }
 
@@ -137,57 +135,69 @@ __device__ __forceinline__ void gemm_mfma(const uint16_t* sX, const uint16_t* sW
 // their fp32 partial sums into a zeroed fp32 output (launches whose tile grid alone
 // would leave most CUs idle: small M).
 template <bool BF16, bool AWQ, int OUT_DT, bool SPLIT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 4))) void gemm_w4a16_kernel(const uint16_t* __restrict__ x,
-                                                         const uint8_t* __restrict__ nib,
-                                                         const float* __restrict__ scales,
-                                                         const float* __restrict__ awq, void* __restrict__ out,
-                                                         int M, int N, int K, int k_split) {
-  __shared__ __align__(16) uint16_t sX[GM_BM * GM_LD];
-  __shared__ __align__(16) uint16_t sW[GM_BN * GM_LD];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_w4a16_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ nib, const float* __restrict__ scales,
+    const float* __restrict__ awq, void* __restrict__ out, int M, int N, int K, int k_split) {
+  // two LDS buffers: slice t+1 is staged (dequantized) into one while the MFMAs of
+  // slice t read the other, so VALU and MFMA work of a wave overlap
+  __shared__ __align__(16) uint16_t sX[2][GM_BM * GM_LD];
+  __shared__ __align__(16) uint16_t sW[2][GM_BN * GM_LD];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves: 32 rows x 64 columns each
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves: 64 rows x 64 columns each
   const int m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
 
-  GemmStage<AWQ> st;
-  const int wrow = tid >> 2, wblk = (tid >> 1) & 1;  // weight row in the tile, block within the slice
+  uint4 rx0, rx1, rx2, rx3, rn;
+  float rs;
+  float4 ra[AWQ ? 8 : 1];
+  const int xr = tid >> 3, xc8 = tid & 7;
+  const int wrow = tid >> 1, wblk = tid & 1;  // weight row in the tile, block within the slice
   const int wn_g = min(n0 + wrow, N - 1);
 
-  f4_t acc[2][4];
+  f16x_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 2; ++j) acc[i][j] = f16x_t{};
 
-  const int fr = lane & 15;
   const int kb = SPLIT ? blockIdx.z * k_split : 0;
   const int ke = SPLIT ? min(K, kb + k_split) : K;
-  // the next slice is in flight while a slice is staged and multiplied; the issue is
-  // unconditional (the last slice re-reads itself), which keeps the staging registers
-  // out of a conditional merge
-  gemm_issue<AWQ>(st, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, kb);
-  for (int k0 = kb; k0 < ke; k0 += GM_BK) {
-    gemm_stage<BF16, AWQ>(st, sX, sW, tid, wrow, wblk);
+  // global loads run two slices ahead of the MFMAs, staging one slice ahead; the
+  // issues are unconditional (slices past the range re-read the last one), which keeps
+  // the staging registers out of a conditional merge
+  const int klast = ke - GM_BK;
+  GEMM_ISSUE(kb);
+  GEMM_STAGE(sX[0], sW[0]);
+  GEMM_ISSUE(min(kb + GM_BK, klast));
+  lds_barrier();
+  for (int k0 = kb; k0 < ke; k0 += 2 * GM_BK) {
+    // slice k0 is in buffer 0; stage k0 + BK into buffer 1 while multiplying buffer 0
+    GEMM_STAGE(sX[1], sW[1]);
+    GEMM_ISSUE(min(k0 + 2 * GM_BK, klast));
+    gemm_mfma<BF16>(sX[0], sW[0], wm, wn, lane, acc);
     lds_barrier();
-    gemm_issue<AWQ>(st, x, nib, scales, awq, tid, m0, M, K, wn_g, wblk, min(k0 + GM_BK, ke - GM_BK));
-    gemm_mfma<BF16>(sX, sW, wm, wn, lane, acc);
-    lds_barrier();  // the tile is rewritten by the next slice
+    // slice k0 + BK is in buffer 1; stage k0 + 2 BK into buffer 0 while multiplying it
+    GEMM_STAGE(sX[0], sW[0]);
+    GEMM_ISSUE(min(k0 + 3 * GM_BK, klast));
+    if (k0 + GM_BK < ke) gemm_mfma<BF16>(sX[1], sW[1], wm, wn, lane, acc);
+    lds_barrier();
   }
 
-  // D[4(l/16) + e][l%16] of tile (i, j)
+  // 32x32 result layout: register r of lane l holds D[8 (r/4) + 4 (l/32) + r%4][l%32]
+  const int fr = lane & 31;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 64 * wn + 16 * j + fr;
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wn + 32 * j + fr;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + 32 * wm + 16 * i + 4 * (lane >> 4) + e;
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < M && n < N) {
           if (SPLIT)
-            atomicAdd((float*)out + (size_t)m * N + n, acc[i][j][e]);
+            atomicAdd((float*)out + (size_t)m * N + n, acc[i][j][r]);
           else
-            store_out<OUT_DT>(out, (size_t)m * N + n, acc[i][j][e]);
+            store_out<OUT_DT>(out, (size_t)m * N + n, acc[i][j][r]);
         }
       }
     }
@@ -197,6 +207,9 @@ __global__ __launch_bounds__(256) void zero_f32_kernel(float4* __restrict__ p, s
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n4) p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
+
+#undef GEMM_ISSUE
+#undef GEMM_STAGE
 
 }  // namespace nve
 
@@ -223,7 +236,7 @@ static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const 
   const int k_split = ((kit + split - 1) / split) * nve::GM_BK;
   const dim3 grid(tn, tm, split);
 #define NVE_GEMM(OD, SP)                                                                                       \
-  hipLaunchKernelGGL((nve::gemm_w4a16_kernel<BF16, AWQ, OD, SP>), grid, dim3(512), 0, s, (const uint16_t*)x, nib, \
+  hipLaunchKernelGGL((nve::gemm_w4a16_kernel<BF16, AWQ, OD, SP>), grid, dim3(256), 0, s, (const uint16_t*)x, nib, \
                      sc, awq, out, M, N, K, k_split)
   if (split > 1) {
     NVE_GEMM(NVE_DT_F32, true);
