@@ -9,9 +9,10 @@ Weights: N(0, 0.02) from a seeded generator, int4 group-quantized on the device 
 the library's Q4_0 quantizer (src/quantize.rs:711-731 semantics).  Activations:
 N(0,1) with 0.5% of channels at +-20 sigma.
 
-One step = one pass over the suite in both precisions (W4A8: 5 activation
-quantizations + 5 GEMV launches, Q/K/V and gate/up each as one grouped launch;
-W4A16: 5 GEMV launches), captured once per weight copy as a HIP
+One step = one pass over the suite in both precisions (W4A8: 5 GEMV launches,
+Q/K/V and gate/up each as one grouped launch, the K = 4096 ones quantizing their
+fp16 input in-kernel and down after one separate quantization launch; W4A16: 5 GEMV
+launches), captured once per weight copy as a HIP
 graph; consecutive steps use different weight copies (>= 1 GB in rotation), so the
 256 MB MALL cannot serve the weights and every byte comes from HBM.
 
@@ -132,6 +133,16 @@ class Step:
                                         out.data_ptr(), odt, n, k, s)
         assert st == 0, st
 
+    def w4a8_x(self, name, ci, x16, s):
+        """W4A8 GEMV that quantizes its fp16 activations itself (one launch)."""
+        n, k = [(n, k) for nm, n, k in SUITE_8B if nm == name][0]
+        nib, sc = self.w[name][ci % len(self.w[name])]
+        out = self.bufs[name][0]
+        odt = 2 if out.dtype == self.t.float32 else 0
+        st = self.L.nve_hip_matvec_w4a8_x(x16.data_ptr(), 0, nib.data_ptr(), sc.data_ptr(), out.data_ptr(), odt, n, k,
+                                          s)
+        assert st == 0, st
+
     def w4a16(self, name, ci, xb, s):
         n, k = [(n, k) for nm, n, k in SUITE_8B if nm == name][0]
         nib, sc = self.w[name][ci % len(self.w[name])]
@@ -148,9 +159,11 @@ class Step:
         for i, name in enumerate(names):
             n = [nn for nm, nn, _ in SUITE_8B if nm == name][0]
             nib, sc = self.w[name][ci % len(self.w[name])]
-            out = self.bufs[name][0 if prec == "w4a8" else 1]
+            out = self.bufs[name][1 if prec == "w4a16" else 0]
             arr[i] = W4Mat(nib.data_ptr(), sc.data_ptr(), None, out.data_ptr(), n)
-        if prec == "w4a8":
+        if prec == "w4a8x":
+            st = self.L.nve_hip_grouped_matvec_w4a8_x(x.data_ptr(), 0, arr, len(names), 0, k, s)
+        elif prec == "w4a8":
             st = self.L.nve_hip_grouped_matvec_w4a8(x.data_ptr(), xs.data_ptr(), arr, len(names), 0, k, s)
         else:
             st = self.L.nve_hip_grouped_matvec_w4a16(x.data_ptr(), 1, arr, len(names), 1, k, s)
@@ -159,19 +172,18 @@ class Step:
     def run(self, ci):
         s = self.t.cuda.current_stream().cuda_stream
         a = self.acts
-        # W4A8: quantize once for q/k/v (src/gpu_layer.rs:658-661; here one grouped
-        # launch), re-quantize for o, once for gate/up (one grouped launch), again for
-        # down, and for the lm_head input.
-        xq, xs = self._quant(a["h16"], 4096, s)
-        self.grouped("w4a8", ("q_proj", "k_proj", "v_proj"), ci, xq, xs, s)
-        xq, xs = self._quant(a["attn16"], 4096, s)
-        self.w4a8("o_proj", ci, xq, xs, s)
-        xq, xs = self._quant(a["h216"], 4096, s)
-        self.grouped("w4a8", ("gate_proj", "up_proj"), ci, xq, xs, s)
+        # W4A8: the reference quantizes once for q/k/v (src/gpu_layer.rs:658-661),
+        # re-quantizes for o, once for gate/up, again for down, and for the lm_head
+        # input.  Here the K = 4096 launches quantize their fp16 input inside the GEMV
+        # (nve_hip_*matvec_w4a8_x, bit-identical; q/k/v and gate/up grouped); down
+        # (K = 14336, where a per-workgroup quantization reads 28 KB of L2 per workgroup)
+        # keeps the separate quantization launch.
+        self.grouped("w4a8x", ("q_proj", "k_proj", "v_proj"), ci, a["h16"], None, s)
+        self.w4a8_x("o_proj", ci, a["attn16"], s)
+        self.grouped("w4a8x", ("gate_proj", "up_proj"), ci, a["h216"], None, s)
         xq, xs = self._quant(a["mid16"], 14336, s)
         self.w4a8("down_proj", ci, xq, xs, s)
-        xq, xs = self._quant(a["final16"], 4096, s)
-        self.w4a8("lm_head", ci, xq, xs, s)
+        self.w4a8_x("lm_head", ci, a["final16"], s)
         # W4A16 (bf16 activations)
         self.grouped("w4a16", ("q_proj", "k_proj", "v_proj"), ci, a["hb"], None, s)
         self.w4a16("o_proj", ci, a["attnb"], s)
@@ -180,15 +192,18 @@ class Step:
         self.w4a16("lm_head", ci, a["finalb"], s)
 
     def step_bytes(self) -> int:
+        """Algorithmic bytes of one step: weights + scales of every GEMV, each launch's
+        activation read (int8 + group scales, or fp16 for the launches that quantize
+        in-kernel / bf16 for W4A16) counted once per launch, outputs, and the separate
+        quantization of the down input (fp16 read, int8 + scales written)."""
         tot = 0
         for name, n, k in SUITE_8B:
             ob = 4 if name == "lm_head" else 2
-            tot += gemv_bytes(n, k, "w4a8", ob) + gemv_bytes(n, k, "w4a16", ob)
-        # grouped launches read their shared activation vector once
-        tot -= 3 * ((4096 + 128 * 4) + 2 * 4096)
-        # activation quantization: read fp16 x, write int8 + f32 scales (5 launches)
-        for k in (4096, 4096, 4096, 14336, 4096):
-            tot += 2 * k + k + (k // 32) * 4
+            tot += weight_bytes(n, k) * 2 + n * ob * 2  # both precisions
+        kq = 14336
+        tot += 4096 * 2 * 4 + (kq + kq // 32 * 4)       # W4A8 inputs: 4 fp16 launches, down int8
+        tot += 2 * kq + kq + kq // 32 * 4               # the down input's quantization
+        tot += 2 * 4096 * 4 + 2 * kq                    # W4A16 inputs (bf16), 5 launches
         return tot
 
 
@@ -625,7 +640,8 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights int4-quantized on device; N(0,1) activations, 0.5% at 20 sigma)",
         "config": {
             "workload": "Llama-3.1-8B layer-shape suite, batch 1, W4A8 + W4A16(bf16): q,k,v,o,gate,up,down,lm_head; "
-                        "one step = both precisions over all shapes incl. 5 activation quantizations",
+                        "one step = both precisions over all shapes incl. the W4A8 activation quantizations "
+                        "(in-kernel for K=4096, one launch for the down input)",
             "weights_in_rotation_GB": rot_gb,
             "step_bytes": sb,
             "graph": "one HIP graph per weight copy, replayed round-robin",

@@ -132,6 +132,18 @@ typedef struct nve_w4_mat {
 int nve_hip_grouped_matvec_w4a8(const int8_t *xq, const float *xq_scales, const nve_w4_mat *mats,
                                 int count, int out_dtype, int K, void *stream);
 
+/* W4A8 GEMV that quantizes its own activations: nve_quantize_f16_q8 and
+ * nve_matvec_w4a8 in one launch (no reference counterpart; the reference issues the two
+ * launches, src/gpu_layer.rs:658-662).  x [K] of x_dtype (F16, BF16 or F32) is
+ * quantized to int8 with group-32 scales inside every workgroup exactly as
+ * nve_hip_quantize_q8 does it, so results are bit-identical to the two-launch sequence.
+ * out_dtype F16 or F32; K <= 16384 (NVE_ERR_TOO_LARGE above). */
+int nve_hip_matvec_w4a8_x(const void *x, int x_dtype, const uint8_t *nibbles, const float *wt_scales,
+                          void *out, int out_dtype, int N, int K, void *stream);
+/* Grouped form (1..3 matrices sharing x and K). */
+int nve_hip_grouped_matvec_w4a8_x(const void *x, int x_dtype, const nve_w4_mat *mats, int count,
+                                  int out_dtype, int K, void *stream);
+
 /* Batched W4A8 (small-batch decode, 1 <= M <= NVE_MAX_M).  xq [M,K]; xs_mode
  * NVE_XS_GROUP32_F32: xq_scales f32 [M, K/32]; NVE_XS_ROW_BF16: bf16 [M].
  * out [M, N] of out_dtype.  M >= 4 runs on int8 MFMA; smaller M on v_dot4. */

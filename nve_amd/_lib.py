@@ -38,6 +38,8 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_qkv_matvec_w4a8": (_i, [_p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
     "nve_hip_grouped_matvec_w4a8": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_grouped_matvec_w4a16": (_i, [_p, _i, _p, _i, _i, _i, _p]),
+    "nve_hip_matvec_w4a8_x": (_i, [_p, _i, _p, _p, _p, _i, _i, _i, _p]),
+    "nve_hip_grouped_matvec_w4a8_x": (_i, [_p, _i, _p, _i, _i, _i, _p]),
     "nve_hip_matvec_w4a8_batched": (_i, [_i, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_w4a8_block_acc": (_i, [_p, _p, _p, _i, _i, _p]),
     "nve_hip_matvec_w4a16": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),

@@ -15,30 +15,39 @@
 //             f64 (src/ops.rs:12-30); a = h (f32 [K]), b = w (bf16 [K]).
 //   SRC_F32:  x_k = a_k (an f32 vector, e.g. silu(gate) * up written by the SwiGLU
 //             epilogue of the gate/up GEMV); b unused.
+//   SRC_F16 / SRC_BF16: x_k = a_k of a 16-bit vector (the W4A8 GEMV that quantizes its
+//             own activations: nve_quantize_f16_q8 + nve_matvec_w4a8 in one launch).
 #pragma once
 
 #include "common.h"
 
 namespace nve {
 
-enum { SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2 };
+enum { SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2, SRC_F16 = 3, SRC_BF16 = 4 };
 
 struct ProdArgs {
-  const float* a;
+  const void* a;
   const void* b;
   float eps;
 };
 
-// E activations (8 or 16) of one staging chunk.
+// E activations (8 or 16) of one staging chunk: f32 sources in a, 16-bit sources in h.
 template <int SRC, int E>
 struct ProdChunk {
-  float4 a[E / 4];
+  static constexpr bool kHalf = SRC == SRC_F16 || SRC == SRC_BF16;
+  float4 a[kHalf ? 1 : E / 4];
+  uint4 h[kHalf ? E / 8 : 1];
   uint4 b[SRC == SRC_NORM ? E / 8 : 1];
 };
 
 template <int SRC, int E>
 __device__ __forceinline__ void prod_issue(ProdChunk<SRC, E>& c, const ProdArgs& p, int chunk, int nchunk) {
   const int i = min(chunk, nchunk - 1);
+  if constexpr (ProdChunk<SRC, E>::kHalf) {
+#pragma unroll
+    for (int t = 0; t < E / 8; ++t) c.h[t] = ((const uint4*)p.a)[i * (E / 8) + t];
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < E / 4; ++t) c.a[t] = ((const float4*)p.a)[i * (E / 4) + t];
   if constexpr (SRC == SRC_NORM) {
@@ -77,6 +86,18 @@ __device__ __forceinline__ double prod_norm_inv(double ss, int K, float eps, dou
 
 template <int SRC, int E>
 __device__ __forceinline__ void prod_values(const ProdChunk<SRC, E>& c, double inv, float (&v)[E]) {
+  if constexpr (ProdChunk<SRC, E>::kHalf) {
+#pragma unroll
+    for (int t = 0; t < E / 8; ++t) {
+      const uint32_t d[4] = {c.h[t].x, c.h[t].y, c.h[t].z, c.h[t].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[8 * t + 2 * e] = SRC == SRC_BF16 ? bf16_bits_to_f32(d[e] & 0xffffu) : f16_bits_to_f32(d[e] & 0xffffu);
+        v[8 * t + 2 * e + 1] = SRC == SRC_BF16 ? bf16_bits_to_f32(d[e] >> 16) : f16_bits_to_f32(d[e] >> 16);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < E / 4; ++t) {
     const float a4[4] = {c.a[t].x, c.a[t].y, c.a[t].z, c.a[t].w};

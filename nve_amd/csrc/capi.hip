@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include "common.h"
+#include "act_producer.h"
 #include "w4_launch.h"
 
 namespace nve_host {
@@ -137,6 +138,41 @@ int nve_hip_grouped_matvec_w4a8(const int8_t* xq, const float* xq_scales, const 
   }
   if (!aligned(xq, 16) || !aligned(xq_scales, 4)) return set_status(NVE_ERR_ALIGN);
   return from_hip(launch_w4a8(xq, xq_scales, s, out_dtype, K, (hipStream_t)stream));
+}
+
+// W4A8 GEMVs that quantize their own activations (nve_quantize_f16_q8 fused into the
+// staging of every workgroup; one staging pass, so K <= 16384).
+static int src_of(int x_dtype) {
+  return x_dtype == NVE_DT_F16 ? nve::SRC_F16 : (x_dtype == NVE_DT_BF16 ? nve::SRC_BF16 : nve::SRC_F32);
+}
+
+int nve_hip_grouped_matvec_w4a8_x(const void* x, int x_dtype, const nve_w4_mat* mats, int count, int out_dtype, int K,
+                                  void* stream) {
+  if (!x || !mats) return set_status(NVE_ERR_NULL);
+  if (count < 1 || count > 3) return set_status(NVE_ERR_SHAPE);
+  if (!dtype_ok(x_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (out_dtype != NVE_DT_F16 && out_dtype != NVE_DT_F32) return set_status(NVE_ERR_DTYPE);
+  W4Segs s{};
+  s.nseg = count;
+  for (int i = 0; i < count; ++i) {
+    int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K);
+    if (st != NVE_OK) return set_status(st);
+    if (!out_aligned(mats[i].out, out_dtype)) return set_status(NVE_ERR_ALIGN);
+    s.nib[i] = mats[i].nibbles;
+    s.sc[i] = mats[i].scales;
+    s.out[i] = mats[i].out;
+    s.n[i] = mats[i].n;
+  }
+  if (K > 16384) return set_status(NVE_ERR_TOO_LARGE);
+  if (!aligned(x, 16)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_w4a8_fused(src_of(x_dtype), false, nve::ProdArgs{x, nullptr, 0.0f}, s, out_dtype, K,
+                                    (hipStream_t)stream));
+}
+
+int nve_hip_matvec_w4a8_x(const void* x, int x_dtype, const uint8_t* nibbles, const float* wt_scales, void* out,
+                          int out_dtype, int N, int K, void* stream) {
+  const nve_w4_mat m = {nibbles, wt_scales, nullptr, out, N};
+  return nve_hip_grouped_matvec_w4a8_x(x, x_dtype, &m, 1, out_dtype, K, stream);
 }
 
 int nve_hip_qkv_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t* q_nib,

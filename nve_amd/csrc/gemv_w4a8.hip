@@ -262,8 +262,20 @@ hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, cons
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32)
     return swiglu ? launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, true>(pa, segs, K, stream)
                   : launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, false>(pa, segs, K, stream);
-  if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
+  if (swiglu) return hipErrorInvalidValue;
+  if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM)
     return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_F32, false>(pa, segs, K, stream);
+  // W4A8 GEMV quantizing its own 16-bit / f32 activations (fp16 or fp32 output)
+#define NVE_QX(SRC)                                                                    \
+  if (src == SRC) {                                                                    \
+    if (out_dt == NVE_DT_F16) return launch_w4a8_fused_t<NVE_DT_F16, SRC, false>(pa, segs, K, stream); \
+    if (out_dt == NVE_DT_F32) return launch_w4a8_fused_t<NVE_DT_F32, SRC, false>(pa, segs, K, stream); \
+    return hipErrorInvalidValue;                                                       \
+  }
+  NVE_QX(nve::SRC_F16)
+  NVE_QX(nve::SRC_BF16)
+  NVE_QX(nve::SRC_F32)
+#undef NVE_QX
   return hipErrorInvalidValue;
 }
 

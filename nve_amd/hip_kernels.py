@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import (DT_BF16, DT_F16, DT_F32, XS_GROUP32_F32, XS_ROW_BF16, check, lib)
+from ._lib import (DT_BF16, DT_F16, DT_F32, XS_GROUP32_F32, XS_ROW_BF16, W4Mat, check, lib)
 
 _DT = {torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.float32: DT_F32}
 
@@ -201,6 +201,27 @@ def q4_repack(q4_blocks: torch.Tensor, n: int, k: int) -> tuple[torch.Tensor, to
     check("nve_hip_q4_repack",
           lib().nve_hip_q4_repack(_dev(q4_blocks, "q4_blocks"), n, k, nib.data_ptr(), sc.data_ptr(), _stream()))
     return nib, sc
+
+
+def matvec_w4a8_x(x: torch.Tensor, nibbles: torch.Tensor, scales: torch.Tensor, n: int, k: int,
+                  out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """quantize_f16_q8 + matvec_w4a8 (src/cuda_kernels.rs:525-573) in one launch: x [K]
+    (fp16 / bf16 / fp32) is quantized inside the GEMV; bit-identical to the pair."""
+    out = torch.empty(n, dtype=out_dtype, device=x.device)
+    check("nve_hip_matvec_w4a8_x",
+          lib().nve_hip_matvec_w4a8_x(_dev(x, "x"), _dt(x), _dev(nibbles, "nibbles"), _dev(scales, "scales"),
+                                      out.data_ptr(), _dt(out), n, k, _stream()))
+    return out
+
+
+def grouped_matvec_w4a8_x(x: torch.Tensor, mats, k: int, out_dtype: torch.dtype = torch.float32) -> list:
+    """Grouped form of matvec_w4a8_x: mats = [(nibbles, scales, n), ...] (1..3) sharing x."""
+    outs = [torch.empty(n, dtype=out_dtype, device=x.device) for _, _, n in mats]
+    arr = (W4Mat * len(mats))(*[W4Mat(_dev(nb, "nibbles"), _dev(sc, "scales"), None, o.data_ptr(), n)
+                               for (nb, sc, n), o in zip(mats, outs)])
+    check("nve_hip_grouped_matvec_w4a8_x",
+          lib().nve_hip_grouped_matvec_w4a8_x(_dev(x, "x"), _dt(x), arr, len(mats), _dt(outs[0]), k, _stream()))
+    return outs
 
 
 def dequant_w4(nibbles: torch.Tensor, scales: torch.Tensor, n: int, k: int, awq: torch.Tensor | None = None,

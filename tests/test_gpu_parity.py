@@ -420,3 +420,49 @@ def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
             q, s = orc.quantize_q8_group(x[r])
             ref = orc.matvec_w4a8_f64(q, s, nib, ws, n, k)
         assert rel_err_floor(y[r], ref) <= TOL_W4A8, r
+
+
+# ---------------------------------------------------------------------------
+# W4A8 GEMV with the activation quantization fused in (nve_hip_matvec_w4a8_x)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,k", [(300, 4096), (4096, 14336), (128256 // 64, 4096), (64, 32)])
+@pytest.mark.parametrize("xdt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("odt", ["f32", "f16"])
+def test_w4a8_fused_quantize_bit_identical(orc, torch_dev, hk, n, k, xdt, odt):
+    """One launch = nve_hip_quantize_q8 + nve_hip_matvec_w4a8, bit for bit; and the
+    int8 codes it forms are the oracle's (checked through the two-launch path)."""
+    torch = torch_dev
+    _, _, nib, ws = _problem(orc, n, k, seed=n + k)
+    x = activations(k, seed=k + 3)
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[xdt]
+    xt = up(torch, x).to(tdt)
+    odt_t = torch.float32 if odt == "f32" else torch.float16
+    tn, tw = up(torch, nib), up(torch, ws)
+    y1 = hk.matvec_w4a8_x(xt, tn, tw, n, k, out_dtype=odt_t)
+    xq, xs = hk.quantize_f16_q8(xt)
+    y2 = torch.empty(n, dtype=odt_t, device="cuda")
+    hk.matvec_w4a8_into(xq, xs, tn, tw, y2, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16 if odt == "f16" else torch.int32),
+                       y2.view(torch.int16 if odt == "f16" else torch.int32))
+    xq_ref, _ = orc.quantize_q8_group(down(xt.float()))
+    assert np.array_equal(down(xq), xq_ref)
+
+
+def test_w4a8_fused_quantize_grouped(orc, torch_dev, hk):
+    torch = torch_dev
+    k = 4096
+    mats, refs = [], []
+    x = up(torch, activations(k, seed=77)).to(torch.float16)
+    xq, xs = hk.quantize_f16_q8(x)
+    for i, n in enumerate((4096, 1024, 1024)):
+        _, _, nib, ws = _problem(orc, n, k, seed=90 + i)
+        tn, tw = up(torch, nib), up(torch, ws)
+        mats.append((tn, tw, n))
+        r = torch.empty(n, dtype=torch.float32, device="cuda")
+        hk.matvec_w4a8_into(xq, xs, tn, tw, r, n, k)
+        refs.append(r)
+    outs = hk.grouped_matvec_w4a8_x(x, mats, k)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        assert torch.equal(o, r)
