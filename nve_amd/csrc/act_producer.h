@@ -17,32 +17,55 @@
 //             epilogue of the gate/up GEMV); b unused.
 //   SRC_F16 / SRC_BF16: x_k = a_k of a 16-bit vector (the W4A8 GEMV that quantizes its
 //             own activations: nve_quantize_f16_q8 + nve_matvec_w4a8 in one launch).
+//   SRC_ATTN2 / SRC_ATTN4: the decode attention output, merged from the partials of 2
+//             or 4 key splits: a = records [split][head] of (m, l, -, -, acc[D]) with
+//             m the running max, l the sum of e^(s - m), acc the unnormalised value
+//             sum; x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s (M = max_s m_s);
+//             i0 = head_dim, i1 = num_heads.
 #pragma once
 
 #include "common.h"
 
 namespace nve {
 
-enum { SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2, SRC_F16 = 3, SRC_BF16 = 4 };
+enum { SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2, SRC_F16 = 3, SRC_BF16 = 4, SRC_ATTN2 = 5, SRC_ATTN4 = 6 };
+
+__host__ __device__ constexpr int attn_splits_of(int src) { return src == SRC_ATTN2 ? 2 : (src == SRC_ATTN4 ? 4 : 0); }
 
 struct ProdArgs {
   const void* a;
   const void* b;
   float eps;
+  int i0, i1;
 };
 
 // E activations (8 or 16) of one staging chunk: f32 sources in a, 16-bit sources in h.
 template <int SRC, int E>
 struct ProdChunk {
   static constexpr bool kHalf = SRC == SRC_F16 || SRC == SRC_BF16;
-  float4 a[kHalf ? 1 : E / 4];
+  static constexpr int kSplits = attn_splits_of(SRC);
+  float4 a[kHalf ? 1 : (kSplits ? kSplits * E / 4 : E / 4)];
   uint4 h[kHalf ? E / 8 : 1];
   uint4 b[SRC == SRC_NORM ? E / 8 : 1];
+  float2 ml[kSplits ? kSplits : 1];
 };
 
 template <int SRC, int E>
 __device__ __forceinline__ void prod_issue(ProdChunk<SRC, E>& c, const ProdArgs& p, int chunk, int nchunk) {
   const int i = min(chunk, nchunk - 1);
+  if constexpr (ProdChunk<SRC, E>::kSplits > 0) {
+    constexpr int S = ProdChunk<SRC, E>::kSplits;
+    const int D = p.i0, H = p.i1;
+    const int e0 = i * E, hd = e0 / D, d0 = e0 % D;
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) {
+      const float* rec = (const float*)p.a + (size_t)(sp * H + hd) * (D + 4);
+      c.ml[sp] = *(const float2*)rec;
+#pragma unroll
+      for (int t = 0; t < E / 4; ++t) c.a[sp * (E / 4) + t] = ((const float4*)(rec + 4 + d0))[t];
+    }
+    return;
+  }
   if constexpr (ProdChunk<SRC, E>::kHalf) {
 #pragma unroll
     for (int t = 0; t < E / 8; ++t) c.h[t] = ((const uint4*)p.a)[i * (E / 8) + t];
@@ -86,6 +109,34 @@ __device__ __forceinline__ double prod_norm_inv(double ss, int K, float eps, dou
 
 template <int SRC, int E>
 __device__ __forceinline__ void prod_values(const ProdChunk<SRC, E>& c, double inv, float (&v)[E]) {
+  if constexpr (ProdChunk<SRC, E>::kSplits > 0) {
+    constexpr int S = ProdChunk<SRC, E>::kSplits;
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) M = fmaxf(M, c.ml[sp].x);
+    float f[S], L = 0.0f;
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) {
+      f[sp] = c.ml[sp].x == -INFINITY ? 0.0f : expf(c.ml[sp].x - M);
+      L = fmaf(f[sp], c.ml[sp].y, L);
+    }
+    const float invL = 1.0f / L;
+#pragma unroll
+    for (int t = 0; t < E / 4; ++t) {
+      float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int sp = 0; sp < S; ++sp) {
+        const float4 a4 = c.a[sp * (E / 4) + t];
+        o[0] = fmaf(f[sp], a4.x, o[0]);
+        o[1] = fmaf(f[sp], a4.y, o[1]);
+        o[2] = fmaf(f[sp], a4.z, o[2]);
+        o[3] = fmaf(f[sp], a4.w, o[3]);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * t + e] = o[e] * invL;
+    }
+    return;
+  }
   if constexpr (ProdChunk<SRC, E>::kHalf) {
 #pragma unroll
     for (int t = 0; t < E / 8; ++t) {

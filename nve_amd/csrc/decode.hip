@@ -162,13 +162,18 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
   m_run = m_new;
 }
 
-template <int D, int OUT>
+// SPLIT > 1 (OUT 3): workgroup (head, sp) takes the tiles t = sp, sp + SPLIT, ... and
+// writes its partial state (m, l, 0, 0, acc[D]) -- acc not yet divided by l -- to
+// out_part[sp][head]; the consumer merges the SPLIT partials (act_producer.h,
+// SRC_ATTN2 / SRC_ATTN4).  A split with no tile writes m = -inf, l = 0, acc = 0.
+template <int D, int OUT, int SPLIT = 1>
 __global__ __launch_bounds__(1024) void attn_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
     int max_seq, float scale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
-    float* __restrict__ out_s) {
+    float* __restrict__ out_s, float* __restrict__ out_part, int xcd_map) {
+  static_assert((OUT == 3) == (SPLIT > 1), "split partials go to out_part");
   using T = AttnTile<D>;
   constexpr int HALF = D / 2;
   __shared__ float s_q[D];
@@ -177,8 +182,20 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   __shared__ float s_m[T::NW], s_l[T::NW];
   __shared__ float s_acc[T::NW * D];
 
-  const int hq = blockIdx.x;
   const int G = num_heads / num_kv_heads;
+  // Workgroups are dealt to the 8 XCDs round-robin (XCD = block % 8), each with its own
+  // L2.  With xcd_map the G query heads of one (kv head, split) -- which read the same
+  // K/V rows -- get block ids 8 apart, so they run on one XCD and share its L2.
+  int hq, sp;
+  if (xcd_map) {
+    const int b = blockIdx.x, x = b % 8, j = b / 8;
+    const int pair = (j / G) * 8 + x;  // (kv head, split) pair
+    hq = (pair % num_kv_heads) * G + j % G;
+    sp = pair / num_kv_heads;
+  } else {
+    hq = blockIdx.x % num_heads;
+    sp = blockIdx.x / num_heads;
+  }
   const int kvh = hq / G;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -190,9 +207,9 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   // past the end re-read the last tile) so the compiler's wait for one buffer never
   // covers a younger one.
   AttnTile<D> b0, b1, b2;
-  attn_issue<D>(b0, kc, vc, cache_base, 0, max_seq, wave, krow, col);
-  attn_issue<D>(b1, kc, vc, cache_base, 1, max_seq, wave, krow, col);
-  attn_issue<D>(b2, kc, vc, cache_base, 2, max_seq, wave, krow, col);
+  attn_issue<D>(b0, kc, vc, cache_base, sp, max_seq, wave, krow, col);
+  attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, max_seq, wave, krow, col);
+  attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, max_seq, wave, krow, col);
   // q, k, v of this head before the position-dependent RoPE rows
   float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
   if (tid < HALF) {
@@ -208,7 +225,9 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   const int pos = min(max(*d_pos, 0), max_seq - 1);
   const int len = pos + 1;
   const int ntiles = (len + T::KT - 1) / T::KT;
-  const int last = ntiles - 1;
+  // this workgroup's tiles: sp + SPLIT * j for j < nt
+  const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
+  const int last = nt - 1;
 
   if (tid < HALF) {
     const float c = rope_cos[(size_t)pos * HALF + tid], sn = rope_sin[(size_t)pos * HALF + tid];
@@ -220,7 +239,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     s_vnew[tid + HALF] = f32_to_bf16_bits(v1);
   }
   lds_barrier();
-  if (hq % G == 0)
+  if (hq % G == 0 && sp == 0)
     for (int i = tid; i < D; i += 1024) {
       kc[cache_base + (size_t)pos * D + i] = s_knew[i];
       vc[cache_base + (size_t)pos * D + i] = s_vnew[i];
@@ -232,15 +251,17 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   float m_run = -INFINITY, l_run = 0.0f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  for (int t = 0; t < ntiles; t += 3) {
-    attn_compute<D>(b0, t, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
-    attn_issue<D>(b0, kc, vc, cache_base, min(t + 3, last), len, wave, krow, col);
-    if (t + 1 < ntiles)
-      attn_compute<D>(b1, t + 1, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
-    attn_issue<D>(b1, kc, vc, cache_base, min(t + 4, last), len, wave, krow, col);
-    if (t + 2 < ntiles)
-      attn_compute<D>(b2, t + 2, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
-    attn_issue<D>(b2, kc, vc, cache_base, min(t + 5, last), len, wave, krow, col);
+  for (int j = 0; j < nt; j += 3) {
+    attn_compute<D>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
+    attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * min(j + 3, last), len, wave, krow, col);
+    if (j + 1 < nt)
+      attn_compute<D>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run,
+                      acc);
+    attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * min(j + 4, last), len, wave, krow, col);
+    if (j + 2 < nt)
+      attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run,
+                      acc);
+    attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * min(j + 5, last), len, wave, krow, col);
   }
   // merge the rows of the wave (same columns), then the waves through LDS
   l_run = stride_sum<T::LPK>(l_run);
@@ -266,6 +287,12 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
       L = fmaf(f, s_l[w], L);
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = fmaf(f, s_acc[w * D + 4 * tid + e], o[e]);
+    }
+    if (OUT == 3) {
+      float* rec = out_part + ((size_t)sp * num_heads + hq) * (D + 4);
+      if (tid == 0) *(float4*)rec = make_float4(M, L, 0.0f, 0.0f);
+      *(float4*)(rec + 4 + 4 * tid) = make_float4(o[0], o[1], o[2], o[3]);
+      return;
     }
     const float invL = 1.0f / L;
 #pragma unroll
@@ -401,8 +428,11 @@ struct DecodeWs {
   float* arg_v;        // [kArgmaxBlocks]
   int* arg_i;          // [kArgmaxBlocks]
   float* logits;       // [V] (head only, when the caller passes no logits buffer)
+  float* part;         // [kMaxAttnSplit][Hq][D + 4] key-split attention partials
   size_t bytes;
 };
+
+constexpr int kMaxAttnSplit = 4;
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -431,6 +461,7 @@ static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
   w.arg_v = (float*)take(nve::kArgmaxBlocks * 4);
   w.arg_i = (int*)take(nve::kArgmaxBlocks * 4);
   w.logits = (float*)take((size_t)(c.vocab > 0 ? c.vocab : 1) * 4);
+  w.part = (float*)take((size_t)kMaxAttnSplit * c.num_heads * (c.head_dim + 4) * 4);
   w.bytes = off;
   return w;
 }
@@ -490,21 +521,39 @@ static hipError_t launch_rmsnorm(const nve_decode_config& c, const float* h, con
 }
 
 static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_io& io, const DecodeWs& ws,
-                                   bool w4a8, hipStream_t s) {
+                                   bool w4a8, int split, hipStream_t s) {
   const float scale = 1.0f / sqrtf((float)c.head_dim);
-#define NVE_ATTN(D, OUT)                                                                                       \
-  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT>), dim3(c.num_heads), dim3(1024), 0, s, ws.q, ws.k, ws.v, \
-                     io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads, c.num_kv_heads,   \
-                     c.max_seq, scale, ws.act_bf16, ws.xq, ws.xs)
+  // (kv head, split) pairs a multiple of 8: each XCD gets whole groups of query heads
+  const int xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1 && !getenv("NVE_ATTN_NOXCD");
+#define NVE_ATTN(D, OUT, S)                                                                                     \
+  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
+                     ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,             \
+                     c.num_kv_heads, c.max_seq, scale, ws.act_bf16, ws.xq, ws.xs, ws.part, xcd_map)
+#define NVE_ATTN_D(D)                    \
+  if (split == 4) NVE_ATTN(D, 3, 4);     \
+  else if (split == 2) NVE_ATTN(D, 3, 2); \
+  else if (w4a8) NVE_ATTN(D, 2, 1);      \
+  else NVE_ATTN(D, 1, 1);
   if (c.head_dim == 64) {
-    if (w4a8) NVE_ATTN(64, 2); else NVE_ATTN(64, 1);
+    NVE_ATTN_D(64)
   } else if (c.head_dim == 128) {
-    if (w4a8) NVE_ATTN(128, 2); else NVE_ATTN(128, 1);
+    NVE_ATTN_D(128)
   } else {
-    if (w4a8) NVE_ATTN(256, 2); else NVE_ATTN(256, 1);
+    NVE_ATTN_D(256)
   }
+#undef NVE_ATTN_D
 #undef NVE_ATTN
   return hipGetLastError();
+}
+
+// Key splits of the fused decode attention (the partials are merged in the o_proj
+// GEMV's staging), chosen from the cache capacity: one workgroup streams about
+// 60 GB/s, so long caches need more workgroups per head, while at a few hundred keys
+// the merge costs more than the split saves.  NVE_ATTN_SPLIT=1/2/4 overrides.
+static int attn_split(const nve_decode_config& c) {
+  const char* e = getenv("NVE_ATTN_SPLIT");
+  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && e[1] == 0) return e[0] - '0';
+  return c.max_seq <= 512 ? 1 : (c.max_seq <= 2048 ? 2 : 4);
 }
 
 // Fused producers in the decode layer (RMSNorm into Q/K/V and gate/up, SiLU * up into
@@ -544,9 +593,16 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
       NVE_TRY(gemv(w4a8, ws, sg, NVE_DT_F32, H, s));
     }
   }
-  // attention writes the o_proj input directly (int8 + scales, or bf16)
-  NVE_TRY(launch_attention(c, io, ws, w4a8, s));
-  NVE_TRY(gemv(w4a8, ws, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
+  // attention writes the o_proj input directly (int8 + scales, or bf16), or, split over
+  // the keys, partials that the o_proj staging merges
+  const int split = fuse ? attn_split(c) : 1;
+  NVE_TRY(launch_attention(c, io, ws, w4a8, split, s));
+  if (split > 1)
+    NVE_TRY(gemv_fused(w4a8, split == 4 ? nve::SRC_ATTN4 : nve::SRC_ATTN2, false,
+                       nve::ProdArgs{ws.part, nullptr, 0.0f, c.head_dim, c.num_heads}, one_seg(w.o, io.hidden),
+                       NVE_DT_F32_ACCUM, QD, s));
+  else
+    NVE_TRY(gemv(w4a8, ws, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
   // FFN sub-layer: norm -> gate/up (one grouped launch) -> silu*up -> down (+h).  Fused:
   // the gate/up launch pairs the rows of both matrices and writes silu(gate) * up
   // (f32 for W4A8, whose down GEMV quantizes it in its staging; bf16 for W4A16).

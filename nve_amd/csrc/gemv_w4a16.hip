@@ -281,13 +281,18 @@ hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt,
 
 // Decode-layer W4A16 GEMVs with a fused producer (act_producer.h), bf16 staging:
 //   NORM, F32          Q/K/V from the residual and the norm weights;
-//   NORM, BF16, swiglu gate/up -> silu(gate) * up rounded to bf16 (the down input).
+//   NORM, BF16, swiglu gate/up -> silu(gate) * up rounded to bf16 (the down input);
+//   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
 hipError_t launch_w4a16_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                               hipStream_t stream) {
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && !swiglu)
     return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, false>(pa, segs, K, stream);
   if (src == nve::SRC_NORM && out_dt == NVE_DT_BF16 && swiglu)
     return launch_w4a16_fused_t<NVE_DT_BF16, nve::SRC_NORM, true>(pa, segs, K, stream);
+  if (src == nve::SRC_ATTN2 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
+    return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, false>(pa, segs, K, stream);
+  if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
+    return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, false>(pa, segs, K, stream);
   return hipErrorInvalidValue;
 }
 

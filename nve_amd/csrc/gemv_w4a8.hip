@@ -256,7 +256,8 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
 // Decode-layer W4A8 GEMVs with a fused producer (act_producer.h):
 //   NORM, F32          Q/K/V from the residual and the norm weights;
 //   NORM, F32, swiglu  gate/up -> silu(gate) * up (f32);
-//   F32, F32_ACCUM     down from that f32 vector, quantized in the staging.
+//   F32, F32_ACCUM     down from that f32 vector, quantized in the staging;
+//   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
 hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                              hipStream_t stream) {
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32)
@@ -265,6 +266,10 @@ hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, cons
   if (swiglu) return hipErrorInvalidValue;
   if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM)
     return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_F32, false>(pa, segs, K, stream);
+  if (src == nve::SRC_ATTN2 && out_dt == NVE_DT_F32_ACCUM)
+    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, false>(pa, segs, K, stream);
+  if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM)
+    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, false>(pa, segs, K, stream);
   // W4A8 GEMV quantizing its own 16-bit / f32 activations (fp16 or fp32 output)
 #define NVE_QX(SRC)                                                                    \
   if (src == SRC) {                                                                    \

@@ -91,12 +91,15 @@ def _run_teacher_forced(torch, m, steps, token0=5):
     return m
 
 
-@pytest.mark.parametrize("fuse", ["1", "0"])
+@pytest.mark.parametrize("fuse,split", [("1", "4"), ("1", "2"), ("1", "1"), ("0", "1")])
 @pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256)])
-def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, monkeypatch):
+def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, split, monkeypatch):
     """Both layer paths: producers fused into the GEMV staging, and standalone
-    RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0)."""
+    RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0); fused attention split over 1, 2 or
+    4 workgroups per head (at 61..66 keys most splits have no tile: their partials are
+    empty and must drop out of the merge)."""
     monkeypatch.setenv("NVE_DECODE_FUSE", fuse)
+    monkeypatch.setenv("NVE_ATTN_SPLIT", split)
     m = _model(torch_dev, heads, kv, d)
     _run_teacher_forced(torch_dev, m, steps=6)  # pos 60..65 crosses a 64-key boundary
 
@@ -146,8 +149,10 @@ def test_decode_3b_shape_smoke(torch_dev, fuse, monkeypatch):
     _run_teacher_forced(torch_dev, m, steps=1)
 
 
-def test_decode_long_cache(torch_dev):
+@pytest.mark.parametrize("split", ["1", "4"])
+def test_decode_long_cache(torch_dev, split, monkeypatch):
     """A cache of 8190+ keys: many tiles per workgroup (256 keys per tile at head_dim
-    64 -> 32 tiles), pos 8190..8192 crosses a tile edge."""
+    64 -> 32 tiles, 8 per split at 4 splits), pos 8190..8192 crosses a tile edge."""
+    monkeypatch.setenv("NVE_ATTN_SPLIT", split)
     m = _model(torch_dev, 4, 2, 64, layers=2, importance=(0.0, 1.0), max_seq=8256, prefill=8190)
     _run_teacher_forced(torch_dev, m, steps=3)
