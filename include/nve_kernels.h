@@ -184,6 +184,18 @@ int nve_hip_qkv_matvec_w4a16(const void *x, int x_dtype, const uint8_t *q_nib,
 int nve_hip_q4_quantize(const void *w, int w_dtype, int N, int K, uint8_t *nibbles,
                         float *scales, void *stream);
 
+/* QuantizedTensor::from_compact_awq (kquant = 0, src/quantize.rs:271-306) and
+ * from_compact_awq_kquant (kquant = 1, 308-346) + extract_for_gpu on the device:
+ * column j of w [N,K] is multiplied by awq[j] (f32) before quantization; with kquant
+ * the block scale is the candidate amax_c / 7 (c-th largest |v|, c < 8, stopping at
+ * the first below 1e-10) that minimises sum_j awq[j]^2 (v_j - q_j scale)^2 (first
+ * minimum; quantize_block_q4_weighted, 741-793), else the plain amax / 7.  Writes the
+ * AWQ inverse scales awq_inv[j] = |awq[j]| > 1e-10 ? 1/awq[j] : 0 when awq_inv is not
+ * NULL (the GEMVs' awq argument).  awq [K] f32 16-byte aligned.  Bit-identical to the
+ * reference for finite inputs. */
+int nve_hip_q4_quantize_awq(const void *w, int w_dtype, const float *awq, int kquant, int N, int K,
+                            uint8_t *nibbles, float *scales, float *awq_inv, void *stream);
+
 /* QuantizedTensor::extract_for_gpu (src/quantize.rs:437-463) on the device: the
  * reference's CPU Q4_0 bytes (20-byte blocks [f32 scale][16 B, byte i = e_2i |
  * e_2i+1 << 4], row-major) -> nibbles in GPU order + scales.  q4_blocks 4-byte

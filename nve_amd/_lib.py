@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_matvec_w4a16": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_qkv_matvec_w4a16": (_i, [_p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
     "nve_hip_q4_quantize": (_i, [_p, _i, _i, _i, _p, _p, _p]),
+    "nve_hip_q4_quantize_awq": (_i, [_p, _i, _p, _i, _i, _i, _p, _p, _p, _p]),
     "nve_hip_q4_repack": (_i, [_p, _i, _i, _p, _p, _p]),
     "nve_hip_dequant_w4": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_gemm_w4a16": (_i, [_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _p]),

@@ -50,6 +50,8 @@ hipError_t launch_q8_rows(const void* x, int xdt, int M, int K, int8_t* xq, uint
                           hipStream_t stream);
 hipError_t launch_q4_quantize(const void* w, int wdt, size_t nblocks, uint8_t* nib, float* scales,
                               hipStream_t stream);
+hipError_t launch_q4_quantize_awq(const void* w, int wdt, size_t nblocks, int bpr, const float* awq, int kquant,
+                                  uint8_t* nib, float* scales, float* awq_inv, hipStream_t stream);
 hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, const float* awq,
                              void* out, int out_dt, int N, int K, hipStream_t s);
 hipError_t launch_dequant_w4(const uint8_t* nib, const float* scales, const float* awq, void* out, int out_dt,
@@ -272,6 +274,18 @@ int nve_hip_q4_quantize(const void* w, int w_dtype, int N, int K, uint8_t* nibbl
   if (!aligned(w, w_dtype == NVE_DT_F32 ? 4 : 2) || !aligned(nibbles, 16) || !aligned(scales, 4))
     return set_status(NVE_ERR_ALIGN);
   return from_hip(launch_q4_quantize(w, w_dtype, (size_t)N * (K / 32), nibbles, scales, (hipStream_t)stream));
+}
+
+int nve_hip_q4_quantize_awq(const void* w, int w_dtype, const float* awq, int kquant, int N, int K,
+                            uint8_t* nibbles, float* scales, float* awq_inv, void* stream) {
+  if (!w || !awq || !nibbles || !scales) return set_status(NVE_ERR_NULL);
+  if (!dtype_ok(w_dtype)) return set_status(NVE_ERR_DTYPE);
+  if (N < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
+  if (!aligned(w, w_dtype == NVE_DT_F32 ? 4 : 2) || !aligned(awq, 16) || !aligned(nibbles, 16) ||
+      !aligned(scales, 4) || (awq_inv && !aligned(awq_inv, 4)))
+    return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_q4_quantize_awq(w, w_dtype, (size_t)N * (K / 32), K / 32, awq, kquant != 0, nibbles,
+                                         scales, awq_inv, (hipStream_t)stream));
 }
 
 int nve_hip_q4_repack(const uint8_t* q4_blocks, int N, int K, uint8_t* nibbles, float* scales,

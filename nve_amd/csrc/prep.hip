@@ -104,18 +104,92 @@ __device__ __forceinline__ float load_w(const void* w, size_t i) {
   return load_act<WDT>(w, i);
 }
 
-template <int WDT>
+// Q4 modes: plain (from_f32 / from_compact), AWQ (from_compact_awq: column j scaled by
+// awq[j] before the plain block quantizer, src/quantize.rs:271-306) and AWQ k-quant
+// (from_compact_awq_kquant, 308-346: the block scale is the candidate amax_c / 7 over
+// the 8 largest |v| that minimises sum_j awq[j]^2 (v_j - deq_j)^2, 741-793).
+enum { Q4_PLAIN = 0, Q4_AWQ = 1, Q4_AWQ_KQUANT = 2 };
+
+template <int WDT, int MODE>
 __global__ __launch_bounds__(256) void q4_quantize_kernel(const void* __restrict__ w, uint8_t* __restrict__ nib,
-                                                          float* __restrict__ scales, size_t nblocks) {
+                                                          float* __restrict__ scales, size_t nblocks,
+                                                          const float* __restrict__ awq, float* __restrict__ awq_inv,
+                                                          int bpr) {
   const size_t blk = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (blk >= nblocks) return;
   float v[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) v[i] = load_w<WDT>(w, blk * 32 + i);
-  float amax = 0.0f;
+  const int col0 = MODE == Q4_PLAIN ? 0 : (int)(blk % (size_t)bpr) * 32;
+  float scale;
+  if constexpr (MODE != Q4_PLAIN) {
 #pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  const float scale = amax > 0.0f ? amax / 7.0f : 0.0f;
+    for (int t = 0; t < 8; ++t) {
+      const float4 a4 = ((const float4*)(awq + col0))[t];
+      v[4 * t] *= a4.x;
+      v[4 * t + 1] *= a4.y;
+      v[4 * t + 2] *= a4.z;
+      v[4 * t + 3] *= a4.w;
+    }
+    // the workgroups of row 0 also write the inverse scales (|s| > 1e-10 ? 1/s : 0)
+    if (awq_inv && blk < (size_t)bpr)
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const float sc = awq[col0 + i];
+        awq_inv[col0 + i] = fabsf(sc) > 1e-10f ? 1.0f / sc : 0.0f;
+      }
+  }
+  if constexpr (MODE == Q4_AWQ_KQUANT) {
+    // Candidate c is the c-th largest |v| (descending sort, src/quantize.rs:746-751):
+    // the element whose rank -- the count of larger values plus equal values at lower
+    // indices -- is c.  Equal values are interchangeable, so any sort order gives the
+    // same candidates (finite inputs).
+    float a[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) a[i] = fabsf(v[i]);
+    float cand[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) cand[c] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      int r = 0;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) r += (a[j] > a[i]) | (j < i && a[j] == a[i]);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) cand[c] = r == c ? a[i] : cand[c];
+    }
+    float best_scale = 0.0f, best_err = 3.40282347e38f;  // f32::MAX
+    bool live = true;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      live = live && !(cand[c] < 1e-10f);  // the reference breaks at the first tiny candidate
+      if (live) {
+        const float cs = cand[c] / 7.0f;
+        const float ci = 1.0f / cs;
+        float err = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          int q = rust_as_i8(roundf(v[j] * ci));
+          q = q < -8 ? -8 : (q > 7 ? 7 : q);
+          const float aj = awq[col0 + j];
+          // (imp * d) * d + err, each product and the sum rounded on its own (Rust
+          // does not contract to FMA)
+          const float d = __fsub_rn(v[j], __fmul_rn((float)q, cs));
+          err = __fadd_rn(err, __fmul_rn(__fmul_rn(__fmul_rn(aj, aj), d), d));
+        }
+        if (err < best_err) {
+          best_err = err;
+          best_scale = cs;
+        }
+      }
+    }
+    scale = best_scale;
+  } else {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    scale = amax > 0.0f ? amax / 7.0f : 0.0f;
+  }
   const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
   int q[32];
 #pragma unroll
@@ -294,16 +368,31 @@ hipError_t launch_q8_rows(const void* x, int xdt, int M, int K, int8_t* xq, uint
   return hipGetLastError();
 }
 
+hipError_t launch_q4_quantize_awq(const void* w, int wdt, size_t nblocks, int bpr, const float* awq, int kquant,
+                                  uint8_t* nib, float* scales, float* awq_inv, hipStream_t stream) {
+  const unsigned grid = (unsigned)((nblocks + 255) / 256);
+#define NVE_Q4Q(DT, MODE)                                                                                      \
+  hipLaunchKernelGGL((nve::q4_quantize_kernel<DT, MODE>), dim3(grid), dim3(256), 0, stream, w, nib, scales, \
+                     nblocks, awq, awq_inv, bpr)
+#define NVE_Q4Q_DT(DT)                                   \
+  if (!awq) NVE_Q4Q(DT, nve::Q4_PLAIN);                  \
+  else if (kquant) NVE_Q4Q(DT, nve::Q4_AWQ_KQUANT);      \
+  else NVE_Q4Q(DT, nve::Q4_AWQ);
+  if (wdt == NVE_DT_F32) {
+    NVE_Q4Q_DT(NVE_DT_F32)
+  } else if (wdt == NVE_DT_BF16) {
+    NVE_Q4Q_DT(NVE_DT_BF16)
+  } else {
+    NVE_Q4Q_DT(NVE_DT_F16)
+  }
+#undef NVE_Q4Q_DT
+#undef NVE_Q4Q
+  return hipGetLastError();
+}
+
 hipError_t launch_q4_quantize(const void* w, int wdt, size_t nblocks, uint8_t* nib, float* scales,
                               hipStream_t stream) {
-  const unsigned grid = (unsigned)((nblocks + 255) / 256);
-  if (wdt == NVE_DT_F32)
-    hipLaunchKernelGGL(nve::q4_quantize_kernel<NVE_DT_F32>, dim3(grid), dim3(256), 0, stream, w, nib, scales, nblocks);
-  else if (wdt == NVE_DT_BF16)
-    hipLaunchKernelGGL(nve::q4_quantize_kernel<NVE_DT_BF16>, dim3(grid), dim3(256), 0, stream, w, nib, scales, nblocks);
-  else
-    hipLaunchKernelGGL(nve::q4_quantize_kernel<NVE_DT_F16>, dim3(grid), dim3(256), 0, stream, w, nib, scales, nblocks);
-  return hipGetLastError();
+  return launch_q4_quantize_awq(w, wdt, nblocks, 1, nullptr, 0, nib, scales, nullptr, stream);
 }
 
 hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, float* scales,

@@ -35,11 +35,19 @@ class GpuW4:
         return GpuW4(nib, sc, awq, n, k)
 
     @staticmethod
-    def quantize(w: torch.Tensor) -> "GpuW4":
-        """Quantize-on-load of a device matrix [N,K] (QuantizedTensor::from_f32 semantics)."""
+    def quantize(w: torch.Tensor, awq: torch.Tensor | None = None, kquant: bool = True) -> "GpuW4":
+        """Quantize-on-load of a device matrix [N,K]: QuantizedTensor::from_f32 /
+        from_compact semantics, or with per-channel AWQ scales awq f32 [K]
+        from_compact_awq_kquant (kquant, the reference's Q4 AWQ load path,
+        src/generic_model.rs:172) / from_compact_awq; the inverse scales become the
+        W4A16 GEMV's awq argument.  As in the reference (src/gpu_layer.rs:656-661),
+        the W4A8 kernels ignore AWQ scales: run AWQ weights on W4A16."""
         n, k = w.shape
-        nib, sc = hk.q4_quantize(w.contiguous())
-        return GpuW4(nib, sc, None, n, k)
+        if awq is None:
+            nib, sc = hk.q4_quantize(w.contiguous())
+            return GpuW4(nib, sc, None, n, k)
+        nib, sc, inv = hk.q4_quantize_awq(w.contiguous(), awq.contiguous(), kquant=kquant)
+        return GpuW4(nib, sc, inv, n, k)
 
     @property
     def nbytes(self) -> int:

@@ -194,6 +194,23 @@ def q4_quantize(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return nib, sc
 
 
+def q4_quantize_awq(w: torch.Tensor, awq: torch.Tensor, kquant: bool = True
+                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """QuantizedTensor::from_compact_awq(_kquant) + extract_for_gpu on the device
+    (src/quantize.rs:271-346): w [N,K] (f32/bf16/f16), awq f32 [K] ->
+    (nibbles, scales, awq_inv f32 [K]); awq_inv is the GEMVs' awq argument."""
+    n, k = w.shape
+    if awq.dtype != torch.float32 or awq.numel() != k:
+        raise ValueError("awq must be float32 [K]")
+    nib = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
+    sc = torch.empty((n, k // 32), dtype=torch.float32, device=w.device)
+    inv = torch.empty(k, dtype=torch.float32, device=w.device)
+    check("nve_hip_q4_quantize_awq",
+          lib().nve_hip_q4_quantize_awq(_dev(w, "w"), _dt(w), _dev(awq, "awq"), int(bool(kquant)), n, k,
+                                        nib.data_ptr(), sc.data_ptr(), inv.data_ptr(), _stream()))
+    return nib, sc, inv
+
+
 def q4_repack(q4_blocks: torch.Tensor, n: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     """extract_for_gpu on the device: reference CPU Q4_0 bytes [N, K/32*20] -> (nibbles, scales)."""
     nib = torch.empty((n, k // 2), dtype=torch.uint8, device=q4_blocks.device)

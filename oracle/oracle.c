@@ -10,6 +10,19 @@
  *                           saturating casts, scale underflow to 0) and the
  *                           reference's own unit tests src/quantize.rs:2234-2252,
  *                           2274-2290 with their inputs and tolerances.
+ *   orc_quantize_block_q4_weighted  hand-derived known answers (an importance-0
+ *                           outlier makes the second candidate exact and win; a
+ *                           single non-zero value reduces to orc_quantize_block_q4;
+ *                           blocks below 1e-10 -> scale 0, nibbles 8) and brute force:
+ *                           the chosen scale's weighted error, re-evaluated in
+ *                           float64, is within rounding of the least over all 8
+ *                           candidates, which are the 8 largest |v| (numpy sort).
+ *   orc_q4_from_f32_awq     awq = 1 reduces to orc_q4_from_f32 (kquant 0) and to
+ *                           the weighted quantizer with unit importance (kquant 1);
+ *                           awq = 2^e scaling commutes exactly (scales x 2^e, same
+ *                           nibbles); the reference unit test src/quantize.rs:2520-
+ *                           2544 (uniform awq 1.5: matvec within 5.0 of the plain
+ *                           one); inv_scales closed form incl. |s| <= 1e-10 -> 0.
  *   orc_q4_from_f32         |deq - w| <= scale/2 and nibble in [1,15] invariants
  *                           on random matrices; byte layout KAT.
  *   orc_q4_to_f32           KAT on one hand-packed block.
@@ -139,6 +152,77 @@ void orc_quantize_block_q4(const float *v, uint8_t *out) {
     b = (int8_t)((b < -8 ? -8 : (b > 7 ? 7 : b)) + 8);
     out[4 + i] = (uint8_t)((uint8_t)a | ((uint8_t)b << 4));
   }
+}
+
+/* src/quantize.rs:741-793: k-quant candidate search.  Candidates are the 8 largest
+ * |v| in descending order (746-751; for finite inputs the order among equal values is
+ * immaterial); the loop stops at the first candidate below 1e-10; the error is summed
+ * in f32 as error += (imp * diff) * diff (no contraction: -ffp-contract=off). */
+void orc_quantize_block_q4_weighted(const float *v, const float *imp, uint8_t *out) {
+  float a[Q4_BLOCK];
+  for (int i = 0; i < Q4_BLOCK; i++) a[i] = fabsf(v[i]);
+  for (int i = 1; i < Q4_BLOCK; i++) { /* insertion sort, descending */
+    float t = a[i];
+    int j = i - 1;
+    while (j >= 0 && a[j] < t) {
+      a[j + 1] = a[j];
+      j--;
+    }
+    a[j + 1] = t;
+  }
+  float best_scale = 0.0f, best_err = 3.40282347e38f; /* f32::MAX */
+  for (int c = 0; c < 8; c++) {
+    float amax = a[c];
+    if (amax < 1e-10f) break;
+    float cs = amax / 7.0f;
+    float ci = 1.0f / cs;
+    float err = 0.0f;
+    for (int j = 0; j < Q4_BLOCK; j++) {
+      int q = orc_rust_f32_as_i8(roundf(v[j] * ci));
+      q = q < -8 ? -8 : (q > 7 ? 7 : q);
+      float deq = (float)q * cs;
+      float diff = v[j] - deq;
+      err += imp[j] * diff * diff;
+    }
+    if (err < best_err) {
+      best_err = err;
+      best_scale = cs;
+    }
+  }
+  float inv = best_scale > 0.0f ? 1.0f / best_scale : 0.0f;
+  memcpy(out, &best_scale, 4);
+  for (int i = 0; i < 16; i++) {
+    int qa = orc_rust_f32_as_i8(roundf(v[2 * i] * inv));
+    int qb = orc_rust_f32_as_i8(roundf(v[2 * i + 1] * inv));
+    qa = (qa < -8 ? -8 : (qa > 7 ? 7 : qa)) + 8;
+    qb = (qb < -8 ? -8 : (qb > 7 ? 7 : qb)) + 8;
+    out[4 + i] = (uint8_t)((uint8_t)qa | ((uint8_t)qb << 4));
+  }
+}
+
+/* src/quantize.rs:271-306 (kquant = 0) and 308-346 (kquant = 1): row_f32[j] *= awq[j],
+ * then the plain or the weighted block quantizer (importance awq[j] * awq[j]);
+ * inv_scales[j] = |awq[j]| > 1e-10 ? 1 / awq[j] : 0 (may be NULL). */
+void orc_q4_from_f32_awq(const float *w, int64_t n, int64_t k, const float *awq, int kquant, uint8_t *data,
+                         float *inv_scales) {
+  int64_t bpr = k / Q4_BLOCK;
+  float *row = (float *)malloc((size_t)k * sizeof(float));
+  float *imp = (float *)malloc((size_t)k * sizeof(float));
+  for (int64_t j = 0; j < k; j++) imp[j] = awq[j] * awq[j];
+  for (int64_t r = 0; r < n; r++) {
+    for (int64_t j = 0; j < k; j++) row[j] = w[r * k + j] * awq[j];
+    for (int64_t b = 0; b < bpr; b++) {
+      uint8_t *o = data + (r * bpr + b) * Q4_BYTES;
+      if (kquant)
+        orc_quantize_block_q4_weighted(row + b * Q4_BLOCK, imp + b * Q4_BLOCK, o);
+      else
+        orc_quantize_block_q4(row + b * Q4_BLOCK, o);
+    }
+  }
+  free(row);
+  free(imp);
+  if (inv_scales)
+    for (int64_t j = 0; j < k; j++) inv_scales[j] = fabsf(awq[j]) > 1e-10f ? 1.0f / awq[j] : 0.0f;
 }
 
 /* src/quantize.rs:347-375 */

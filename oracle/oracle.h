@@ -38,6 +38,9 @@ uint16_t orc_f32_to_bf16(float f);
  * [f32 LE scale][16 bytes, byte i = q[2i] | q[2i+1] << 4]. */
 void orc_quantize_block_q4(const float *v32, uint8_t *out20);
 /* QuantizedTensor::from_f32, src/quantize.rs:347-375 (K % 32 == 0). */
+void orc_quantize_block_q4_weighted(const float *v, const float *imp, uint8_t *out);
+void orc_q4_from_f32_awq(const float *w, int64_t n, int64_t k, const float *awq, int kquant, uint8_t *data,
+                         float *inv_scales);
 void orc_q4_from_f32(const float *w, int64_t n, int64_t k, uint8_t *data);
 /* QuantizedTensor::to_f32_vec, src/quantize.rs:396-426 (awq_inv nullable). */
 void orc_q4_to_f32(const uint8_t *data, int64_t n, int64_t k, const float *awq_inv,

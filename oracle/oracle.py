@@ -42,6 +42,8 @@ def lib() -> C.CDLL:
         L.orc_f32_to_bf16.restype = C.c_uint16
         L.orc_quantize_block_q4.argtypes = [p, p]
         L.orc_q4_from_f32.argtypes = [p, i64, i64, p]
+        L.orc_quantize_block_q4_weighted.argtypes = [p, p, p]
+        L.orc_q4_from_f32_awq.argtypes = [p, i64, i64, p, C.c_int, p, p]
         L.orc_q4_to_f32.argtypes = [p, i64, i64, p, p]
         L.orc_extract_for_gpu.argtypes = [p, i64, i64, p, p]
         L.orc_q4_dot_row_scalar.argtypes = [p, p, i64]
@@ -90,6 +92,27 @@ def q4_from_f32(w) -> np.ndarray:
     out = np.zeros((n, k // 32 * 20), np.uint8)
     lib().orc_q4_from_f32(_ptr(w), n, k, _ptr(out))
     return out
+
+
+def quantize_block_q4_weighted(v32, imp32) -> np.ndarray:
+    """src/quantize.rs:741-793 -> 20 bytes."""
+    v, imp = _c(v32, np.float32), _c(imp32, np.float32)
+    assert v.size == 32 and imp.size == 32
+    out = np.zeros(20, np.uint8)
+    lib().orc_quantize_block_q4_weighted(_ptr(v), _ptr(imp), _ptr(out))
+    return out
+
+
+def q4_from_f32_awq(w, awq, kquant: bool) -> tuple[np.ndarray, np.ndarray]:
+    """QuantizedTensor::from_compact_awq (kquant False, src/quantize.rs:271-306) /
+    from_compact_awq_kquant (True, 308-346) on the f32 rows -> (bytes, inv_scales)."""
+    w, awq = _c(w, np.float32), _c(awq, np.float32)
+    n, k = w.shape
+    assert k % 32 == 0 and awq.size == k
+    out = np.zeros((n, k // 32 * 20), np.uint8)
+    inv = np.zeros(k, np.float32)
+    lib().orc_q4_from_f32_awq(_ptr(w), n, k, _ptr(awq), int(bool(kquant)), _ptr(out), _ptr(inv))
+    return out, inv
 
 
 def q4_to_f32(data, n, k, awq_inv=None) -> np.ndarray:

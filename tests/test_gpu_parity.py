@@ -274,6 +274,57 @@ def test_q4_quantize_device_bit_exact(orc, torch_dev, hk, wdt):
     assert np.array_equal(down(sc).view(np.uint32), sc_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("kquant", [False, True])
+@pytest.mark.parametrize("wdt", ["f32", "bf16", "f16"])
+def test_q4_quantize_awq_device_bit_exact(orc, torch_dev, hk, wdt, kquant):
+    """from_compact_awq(_kquant) + extract_for_gpu on the device against the oracle's
+    restatement (src/quantize.rs:271-346, 741-793) on the same weights."""
+    torch = torch_dev
+    n, k = 131, 1024
+    w = weights(n, k, seed=31, std=0.5)
+    rng = np.random.default_rng(32)
+    awq = rng.uniform(0.25, 4.0, k).astype(np.float32)
+    awq[5], awq[40] = 0.0, -2.0  # a dead channel (inverse 0) and a negative scale
+    # special blocks in row 0: a constant block with a dead channel (awq 0 zeroes
+    # both the value and its importance), a ramp with unit awq, a tiny block (every
+    # |v| < 1e-10: no candidate, scale 0)
+    awq[64:96] = 1.0
+    w[0, 0:32] = 3.5
+    w[0, 5] = 7.0
+    w[0, 32:64] = (np.arange(32) - 16) * 0.5
+    w[0, 64:96] = 5e-11 if wdt == "f32" else 0.0
+    w[1, ::7] *= 20.0  # outliers
+    if wdt == "f32":
+        wt, wv = up(torch, w), w
+    elif wdt == "bf16":
+        wv = to_bf16(w)
+        wt = up(torch, wv).to(torch.bfloat16)
+    else:
+        wv = to_f16(w)
+        wt = up(torch, w.astype(np.float16))
+    nib, sc, inv = hk.q4_quantize_awq(wt, up(torch, awq), kquant=kquant)
+    data_ref, inv_ref = orc.q4_from_f32_awq(wv, awq, kquant)
+    nib_ref, sc_ref = orc.extract_for_gpu(data_ref, n, k)
+    assert np.array_equal(down(nib), nib_ref)
+    assert np.array_equal(down(sc).view(np.uint32), sc_ref.view(np.uint32))
+    assert np.array_equal(down(inv).view(np.uint32), inv_ref.view(np.uint32))
+
+
+def test_q4_quantize_awq_feeds_w4a16_gemv(orc, torch_dev, hk):
+    """AWQ end to end: the device-quantized weights and inverse scales through the
+    W4A16 GEMV against the float64 dequantized product (bar 2e-3)."""
+    torch = torch_dev
+    n, k = 512, 2048
+    w = weights(n, k, seed=41, std=0.02)
+    awq = np.random.default_rng(42).uniform(0.5, 2.0, k).astype(np.float32)
+    nib, sc, inv = hk.q4_quantize_awq(up(torch, w), up(torch, awq), kquant=True)
+    x = activations(k, seed=43)
+    xb = to_bf16(x)
+    y = down(hk.fused_matvec_w4a16(up(torch, xb).to(torch.bfloat16), nib, sc, inv, n, k, out_dtype=torch.float32))
+    ref = orc.matvec_w4a16_f64(xb, down(nib), down(sc), n, k, awq=down(inv))
+    assert rel_err_floor(y, ref) <= 2e-3
+
+
 def test_q4_repack_device_bit_exact(orc, torch_dev, hk):
     torch = torch_dev
     n, k = 129, 4096
