@@ -80,21 +80,29 @@ __global__ __launch_bounds__(256) void w4a8_batched_dot4_kernel(int M, const int
 // ---------------------------------------------------------------------------
 // int8 MFMA kernel (M >= 4).
 //
-// Workgroup = one 16-row tile of W, KW waves splitting K (wave w takes block quads
-// w, w+KW, ...; U quads' loads are issued together).  Per quad (4 consecutive
-// 32-weight blocks) lane (n = lane%16,
-// g = lane/16) loads the whole 16-byte block 4q+g of row n (one dwordx4; a wave
-// instruction reads 16 rows x 64 contiguous bytes).  Two permlane32 swaps and two
-// permlane16 swaps transpose the 4x4 (lane group x dword) grid so that register j
-// holds, in lane (n, g), dword g of block 4q+j: the 8 weights that lane contributes
-// to the MFMA over block 4q+j (low nibbles = elements 4g..4g+3, high nibbles =
-// elements 16+4g..16+4g+3).  Nibbles become signed int8 (nib - 8) in registers; the
-// activations are loaded the same way (lane (m, g) reads the 32 bytes of block 4q+g
-// of row m, two dwordx4) and transposed, so the activation operand of lane (m, g)
-// holds xq[m] at the same 8 positions,
-// and one v_mfma_i32_16x16x32_i8 per block gives the exact int32 accumulators
-// D[n][m] for all 16 activation rows (rows m >= M are zero).  The fp32 epilogue
-// applies ws[n,b] * xs[m,b] per block; the KW partial sums meet in LDS.
+// The activation rows are the A operand of v_mfma_i32_16x16x32_i8 (rows i) and a
+// 16-row weight tile the B operand (columns n), one 32-weight block per MFMA, so a
+// block's output D[i][n] lands with weight row n = lane % 16 in every lane and the
+// block's weight scale is one value per lane.  Nibbles enter the MFMA raw (0..15 is
+// a valid int8); the -8 offset is the accumulator input C[i][.] = -8 * sum_k xq[i, k],
+// itself one MFMA of the activation operand with a B operand of all -8 bytes: the
+// int32 block accumulators are exact, as in the one-row kernels.
+//
+// Memory access: the operand layout (lane = (row % 16, k group)) puts 4 different
+// rows in 4 consecutive lanes, and the texture path serves a wave load one 64-byte
+// piece per 4 consecutive lanes only when those lanes read 64 contiguous bytes;
+// loaded in operand order, every lane costs a separate cache access (measured 17x
+// the accesses of the one-row GEMV on the same bytes).  So every load is issued in
+// row-major lane order -- lane (r = lane / 4, p = lane % 4) reads piece p of row r,
+// 16 rows x 64 contiguous bytes per instruction -- and the registers are moved to the
+// operand lanes with ds_bpermute (through the LDS crossbar, no LDS storage), then the
+// 4x4 (lane group x dword) transpose of two permlane32 + two permlane16 swaps.
+//
+// Activation row m sits in A row i = 4 (m % 4) + m / 4, so D row 4g + e (lane group
+// g, element e) is activation row 4e + g: for M <= 4 only element 0 of each lane is
+// live, for M <= 8 elements 0-1 (EU = ceil(M / 4) elements are scaled and summed).
+// A workgroup owns T weight tiles; its KS waves take the quads (4 blocks) q = wave,
+// wave + KS, ... of K and meet in LDS.
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void transpose4(uint32_t& c0, uint32_t& c1, uint32_t& c2, uint32_t& c3) {
@@ -113,106 +121,158 @@ __device__ __forceinline__ void transpose4(uint32_t& c0, uint32_t& c1, uint32_t&
   c3 = s23[1];
 }
 
-__device__ __forceinline__ long a_operand(uint32_t d) {
-  const uint32_t lo = s8_from_nib(d & 0x0F0F0F0Fu);
-  const uint32_t hi = s8_from_nib((d >> 4) & 0x0F0F0F0Fu);
-  return (long)(((unsigned long)hi << 32) | lo);
+__device__ __forceinline__ uint32_t lane_fetch(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+__device__ __forceinline__ uint4 lane_fetch4(uint4 v, int src_lane) {
+  return make_uint4(lane_fetch(v.x, src_lane), lane_fetch(v.y, src_lane), lane_fetch(v.z, src_lane),
+                    lane_fetch(v.w, src_lane));
 }
 
-template <int OUT_DT, int XS_MODE, int KW, int U>
-__global__ __launch_bounds__(64 * KW) void w4a8_batched_mfma_kernel(int M, const int8_t* __restrict__ xq,
+// One quad of K: activations (two 16-byte halves of block 4q+p of activation row r)
+// and, per tile, weights (block 4q+p of weight row r) and the quad's 4 weight scales,
+// all in the row-major load layout.
+template <int T>
+struct BQuad {
+  uint4 xa, xb;
+  uint4 w[T];
+  float4 sc[T];
+};
+
+template <int T>
+__device__ __forceinline__ void bquad_issue(BQuad<T>& st, const uint4* xrow, const uint4* const (&wrow)[T],
+                                            const float* const (&srow)[T], bool vec_sc, int q, int nq, int nb,
+                                            int p) {
+  q = min(q, nq - 1);
+  const int bl = min(4 * q + p, nb - 1);
+  st.xa = xrow[2 * bl];
+  st.xb = xrow[2 * bl + 1];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    st.w[t] = ld_stream(wrow[t] + bl);
+    if (vec_sc) {
+      st.sc[t] = ((const float4*)srow[t])[q];
+    } else {
+      st.sc[t].x = srow[t][min(4 * q + 0, nb - 1)];
+      st.sc[t].y = srow[t][min(4 * q + 1, nb - 1)];
+      st.sc[t].z = srow[t][min(4 * q + 2, nb - 1)];
+      st.sc[t].w = srow[t][min(4 * q + 3, nb - 1)];
+    }
+  }
+}
+
+template <int XS_MODE, int T, int EU>
+__device__ __forceinline__ void bquad_compute(const BQuad<T>& st, int q, int nb, bool m_ok, int src_w, int src_x,
+                                              const float* xs_g, int M, int g, float (&acc)[T][EU]) {
+  constexpr long kMinus8 = (long)0xF8F8F8F8F8F8F8F8ull;
+  // A operand: lane (i, g) <- load lane (m(i), g); then dword g of each block's halves
+  const uint4 xa = lane_fetch4(st.xa, src_x), xb = lane_fetch4(st.xb, src_x);
+  uint32_t l0 = xa.x, l1 = xa.y, l2 = xa.z, l3 = xa.w;
+  uint32_t h0 = xb.x, h1 = xb.y, h2 = xb.z, h3 = xb.w;
+  transpose4(l0, l1, l2, l3);
+  transpose4(h0, h1, h2, h3);
+  const uint32_t lj[4] = {l0, l1, l2, l3};
+  const uint32_t hj[4] = {h0, h1, h2, h3};
+  long a[4];
+  v4i_t cm[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a[j] = m_ok ? (long)(((unsigned long)hj[j] << 32) | lj[j]) : 0L;
+    const v4i_t z = {0, 0, 0, 0};
+    cm[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], kMinus8, z, 0, 0, 0);
+  }
+  // group scales xs[m = 4e + g][4q + j]
+  float xsv[4][EU];
+  if (XS_MODE == NVE_XS_GROUP32_F32) {
+#pragma unroll
+    for (int e = 0; e < EU; ++e) {
+      const float* r = xs_g + (size_t)min(4 * e + g, M - 1) * nb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xsv[j][e] = r[min(4 * q + j, nb - 1)];
+    }
+  }
+  const bool full = 4 * q + 3 < nb;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint4 w = lane_fetch4(st.w[t], src_w);
+    uint32_t c0 = w.x, c1 = w.y, c2 = w.z, c3 = w.w;
+    transpose4(c0, c1, c2, c3);
+    const uint32_t cj[4] = {c0, c1, c2, c3};
+    const uint4 sw = lane_fetch4(make_uint4(__float_as_uint(st.sc[t].x), __float_as_uint(st.sc[t].y),
+                                            __float_as_uint(st.sc[t].z), __float_as_uint(st.sc[t].w)),
+                                 src_w);
+    float scj[4] = {__uint_as_float(sw.x), __uint_as_float(sw.y), __uint_as_float(sw.z), __uint_as_float(sw.w)};
+    // blocks past the end (last quad only) were loaded clamped: weight them 0
+#pragma unroll
+    for (int j = 1; j < 4; ++j) scj[j] = (full || 4 * q + j < nb) ? scj[j] : 0.0f;
+    v4i_t d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = cj[j] & 0x0F0F0F0Fu, hi = (cj[j] >> 4) & 0x0F0F0F0Fu;
+      d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], (long)(((unsigned long)hi << 32) | lo), cm[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < EU; ++e) {
+        const float f = XS_MODE == NVE_XS_GROUP32_F32 ? scj[j] * xsv[j][e] : scj[j];
+        acc[t][e] = fmaf(f, (float)d[j][e], acc[t][e]);
+      }
+  }
+}
+
+template <int OUT_DT, int XS_MODE, int KS, int T, int EU>
+__global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_kernel(int M, const int8_t* __restrict__ xq,
                                                                     const void* __restrict__ xs,
                                                                     const uint8_t* __restrict__ nib,
                                                                     const float* __restrict__ ws,
-                                                                    void* __restrict__ out, int N, int K) {
-  __shared__ float s_ws[KW][U][4][16];  // per wave: scales of the current quads, [u][block j][row n]
-  __shared__ float s_red[KW][16][17];   // per wave partial sums [n][m] (+1 pad)
+                                                                    void* __restrict__ out, int N, int K,
+                                                                    int vec_sc) {
+  __shared__ float s_red[KS][T * 16][4 * EU + 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nl = lane & 15;  // weight row within the tile (A operand) / activation row m (B, D)
-  const int g = lane >> 4;   // k group
-  const int row0 = blockIdx.x * 16;
+  const int nl = lane & 15, g = lane >> 4;  // operand layout
+  const int lr = lane >> 2, lp = lane & 3;  // load layout: 4 consecutive lanes per row
+  const int row0 = blockIdx.x * (16 * T);
   const int nb = K >> 5;
   const int nq = (nb + 3) >> 2;
-  const int row = min(row0 + nl, N - 1);
-  const uint4* wrow = (const uint4*)(nib + (size_t)row * (size_t)(K >> 1));
-  const float* srow = ws + (size_t)row * nb;
-  const int m = nl;
-  const int mc = min(m, M - 1);
-  const bool m_ok = m < M;
-  const uint4* xrow = (const uint4*)(xq + (size_t)mc * K);  // 2 x 16 B per block
-
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int q0 = wave; q0 < nq; q0 += KW * U) {
-    // All loads of the U quads first (clamped, unconditional).  Lane (n, g) loads
-    // weight block 4q+g of row n; lane (m, g) loads the 32 activation bytes of block
-    // 4q+g of row m; both grids are transposed to MFMA operand order below.
-    uint4 w[U], xa[U], xb[U];
-    float sc[U], xsv[U][4];
+  const size_t row_bytes = (size_t)(K >> 1);
+  const uint4* wrow[T];
+  const float* srow[T];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int q = min(q0 + KW * u, nq - 1);
-      const int bl = min(4 * q + g, nb - 1);
-      w[u] = ld_stream(wrow + bl);
-      sc[u] = ld_stream(srow + bl);
-      xa[u] = xrow[2 * bl];
-      xb[u] = xrow[2 * bl + 1];
-      if (XS_MODE == NVE_XS_GROUP32_F32) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xsv[u][j] = ((const float*)xs)[(size_t)mc * nb + min(4 * q + j, nb - 1)];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) s_ws[wave][u][g][nl] = sc[u];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int bq = 4 * (q0 + KW * u);
-      uint32_t c0 = w[u].x, c1 = w[u].y, c2 = w[u].z, c3 = w[u].w;
-      transpose4(c0, c1, c2, c3);
-      // activations: dword i of a block holds elements 4i..4i+3; lane g needs dwords
-      // g (elements 4g..) and 4+g (elements 16+4g..) of each block of the quad
-      uint32_t l0 = xa[u].x, l1 = xa[u].y, l2 = xa[u].z, l3 = xa[u].w;
-      uint32_t h0 = xb[u].x, h1 = xb[u].y, h2 = xb[u].z, h3 = xb[u].w;
-      transpose4(l0, l1, l2, l3);
-      transpose4(h0, h1, h2, h3);
-      const uint32_t cj[4] = {c0, c1, c2, c3};
-      const uint32_t lj[4] = {l0, l1, l2, l3};
-      const uint32_t hj[4] = {h0, h1, h2, h3};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (bq + j < nb) {  // wave-uniform
-          const long a = a_operand(cj[j]);
-          const long bx = m_ok ? (long)(((unsigned long)hj[j] << 32) | lj[j]) : 0L;
-          v4i_t d = {0, 0, 0, 0};
-          d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bx, d, 0, 0, 0);
-          const float4 wsv = *(const float4*)&s_ws[wave][u][j][4 * g];  // rows 4g..4g+3
-          const float xsf = XS_MODE == NVE_XS_GROUP32_F32 ? xsv[u][j] : 1.0f;
-          acc[0] = fmaf(wsv.x * xsf, (float)d[0], acc[0]);
-          acc[1] = fmaf(wsv.y * xsf, (float)d[1], acc[1]);
-          acc[2] = fmaf(wsv.z * xsf, (float)d[2], acc[2]);
-          acc[3] = fmaf(wsv.w * xsf, (float)d[3], acc[3]);
-        }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  for (int t = 0; t < T; ++t) {
+    const int r = min(row0 + 16 * t + lr, N - 1);
+    wrow[t] = (const uint4*)(nib + (size_t)r * row_bytes);
+    srow[t] = ws + (size_t)r * nb;
   }
-  // D layout: lane holds column m = lane%16, rows 4g..4g+3.
+  const uint4* xrow = (const uint4*)(xq + (size_t)min(lr, M - 1) * K);
+  const int am = 4 * (nl & 3) + (nl >> 2);  // activation row of A row nl
+  const bool m_ok = am < M;
+  const int src_w = 4 * nl + g;  // load lane holding (weight row nl, piece g)
+  const int src_x = 4 * am + g;  // load lane holding (activation row am, piece g)
+  float acc[T][EU];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) s_red[wave][4 * g + v][m] = acc[v];
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < EU; ++e) acc[t][e] = 0.0f;
+  for (int q = wave; q < nq; q += KS) {
+    BQuad<T> st;
+    bquad_issue<T>(st, xrow, wrow, srow, vec_sc != 0, q, nq, nb, lp);
+    bquad_compute<XS_MODE, T, EU>(st, q, nb, m_ok, src_w, src_x, (const float*)xs, M, g, acc);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < EU; ++e) s_red[wave][16 * t + nl][4 * e + g] = acc[t][e];
   __syncthreads();
-  for (int t = threadIdx.x; t < 256; t += 64 * KW) {
-    const int n = t >> 4, mm = t & 15;
+  for (int i = threadIdx.x; i < T * 16 * 4 * EU; i += 64 * KS) {
+    const int mm = i / (16 * T), r = i % (16 * T);
     float y = 0.0f;
 #pragma unroll
-    for (int w2 = 0; w2 < KW; ++w2) y += s_red[w2][n][mm];
-    if (mm < M && row0 + n < N) {
+    for (int w2 = 0; w2 < KS; ++w2) y += s_red[w2][r][mm];
+    if (mm < M && row0 + r < N) {
       if (XS_MODE == NVE_XS_ROW_BF16) y *= bf16_bits_to_f32(((const uint16_t*)xs)[mm]);
-      store_out<OUT_DT>(out, (size_t)mm * N + row0 + n, y);
+      store_out<OUT_DT>(out, (size_t)mm * N + row0 + r, y);
     }
   }
 }
@@ -225,12 +285,27 @@ namespace nve_host {
 // v_dot4 kernels (nve_hip_set_gemv_policy(NVE_GEMV_ONESHOT, ...)).
 static bool batched_use_mfma() { return gemv_policy() != NVE_GEMV_ONESHOT; }
 
-template <int OUT_DT, int XS, int KW>
+// 16 waves per workgroup (the K quads are dealt round-robin); two 16-row tiles per
+// workgroup while that still leaves at least 256 workgroups, else one.
+template <int OUT_DT, int XS, int EU>
 static hipError_t launch_mfma(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
                               void* out, int N, int K, hipStream_t stream) {
-  hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, KW, 4>), dim3((N + 15) / 16), dim3(64 * KW), 0,
-                     stream, M, xq, xs, nib, ws, out, N, K);
+  const int vec_sc = (K % 128 == 0) && aligned(ws, 16);
+  if ((N + 31) / 32 >= 256)
+    hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, 16, 2, EU>), dim3((N + 31) / 32), dim3(1024), 0,
+                       stream, M, xq, xs, nib, ws, out, N, K, vec_sc);
+  else
+    hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, 16, 1, EU>), dim3((N + 15) / 16), dim3(1024), 0,
+                       stream, M, xq, xs, nib, ws, out, N, K, vec_sc);
   return hipGetLastError();
+}
+
+template <int OUT_DT, int XS>
+static hipError_t launch_mfma_m(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
+                                void* out, int N, int K, hipStream_t stream) {
+  if (M <= 4) return launch_mfma<OUT_DT, XS, 1>(M, xq, xs, nib, ws, out, N, K, stream);
+  if (M <= 8) return launch_mfma<OUT_DT, XS, 2>(M, xq, xs, nib, ws, out, N, K, stream);
+  return launch_mfma<OUT_DT, XS, 4>(M, xq, xs, nib, ws, out, N, K, stream);
 }
 
 template <int OUT_DT>
@@ -238,14 +313,9 @@ static hipError_t launch_batched_o(int M, const int8_t* xq, const void* xs, int 
                                    const uint8_t* nib, const float* ws, void* out, int N, int K,
                                    hipStream_t stream) {
   if (M >= 4 && batched_use_mfma()) {
-    // 8 waves per tile when there are too few 16-row tiles to give every CU two
-    // workgroups, 4 otherwise.
-    const bool wide = (N + 15) / 16 < 512;
     if (xs_mode == NVE_XS_ROW_BF16)
-      return wide ? launch_mfma<OUT_DT, NVE_XS_ROW_BF16, 8>(M, xq, xs, nib, ws, out, N, K, stream)
-                  : launch_mfma<OUT_DT, NVE_XS_ROW_BF16, 4>(M, xq, xs, nib, ws, out, N, K, stream);
-    return wide ? launch_mfma<OUT_DT, NVE_XS_GROUP32_F32, 8>(M, xq, xs, nib, ws, out, N, K, stream)
-                : launch_mfma<OUT_DT, NVE_XS_GROUP32_F32, 4>(M, xq, xs, nib, ws, out, N, K, stream);
+      return launch_mfma_m<OUT_DT, NVE_XS_ROW_BF16>(M, xq, xs, nib, ws, out, N, K, stream);
+    return launch_mfma_m<OUT_DT, NVE_XS_GROUP32_F32>(M, xq, xs, nib, ws, out, N, K, stream);
   }
   const dim3 grid((N + 3) / 4);
   if (xs_mode == NVE_XS_ROW_BF16)

@@ -456,8 +456,9 @@ def test_dispatch_project(orc, torch_dev, hk, monkeypatch):
                                  (4096, 14336)])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
-    """M >= 4 runs on the int8 MFMA kernel: ragged N, K with a partial last block quad,
-    both wave splits (N/16 below and above 512 tiles)."""
+    """M >= 4 runs on the int8 MFMA kernel: ragged N, K with a partial last block quad
+    (K % 128 != 0: scalar scale loads), one and two 16-row tiles per workgroup (8200
+    rows), every live-element count (M = 4, 5-8, 13-16)."""
     torch = torch_dev
     _, _, nib, ws = _problem(orc, n, k, seed=m * 7 + n)
     x = to_bf16(activations(k, seed=300 + m, m=m))
