@@ -315,7 +315,7 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
 def batched_sweep(torch, L, weights, launches_per_graph: int = 40):
     """W4A8 at M in {1,2,4,8,16} activation rows (per-row absmax
     int8, bf16 scales) on the 8B gate (14336x4096) and down (4096x14336) shapes.
-    M >= 4 runs on int8 MFMA (v_mfma_i32_16x16x32_i8, 16 activation columns per
+    M >= 2 runs on int8 MFMA (v_mfma_i32_16x16x32_i8, 16 activation columns per
     instruction, so the issued MFMA work is 2*16*N*K per launch whatever M is)."""
     import numpy as np
     rows = {}
@@ -344,8 +344,8 @@ def batched_sweep(torch, L, weights, launches_per_graph: int = 40):
             rec = {"M": m, "N": n, "K": k, "us": round(us, 3), "GBs": round(b / us / 1e3, 1),
                    "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                    "useful_int8_TOPs": round(2 * m * n * k / us / 1e6, 2),
-                   "kernel": "mfma_i32_16x16x32_i8" if m >= 4 else "v_dot4"}
-            if m >= 4:
+                   "kernel": "mfma_i32_16x16x32_i8" if m >= 2 else "v_dot4"}
+            if m >= 2:
                 issued = 2 * 16 * n * k / us / 1e6
                 rec["issued_mfma_TOPs"] = round(issued, 2)
                 rec["mfma_util_vs_5000_TOPs"] = round(issued / 5000.0, 4)

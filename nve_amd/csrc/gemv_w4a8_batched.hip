@@ -5,7 +5,7 @@
 // or the per-row bf16 scale (per-token mode, applied once per row: the sum over
 // blocks is formed with ws only and multiplied by the row scale at the end).
 //
-// v_dot4 kernel (M < 4): one wave per output row, lane l owns
+// v_dot4 kernel (M = 1, or any M under NVE_GEMV_ONESHOT): one wave per output row, lane l owns
 // blocks l, l+64, ...; the nibbles are turned into signed int8 (nib - 8) once per
 // block with (t + 0x78787878) ^ 0x80808080 (no carries cross bytes for t <= 15), and
 // every activation row reuses them through 8 v_dot4_i32_i8.
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void w4a8_batched_dot4_kernel(int M, const int
 }
 
 // ---------------------------------------------------------------------------
-// int8 MFMA kernel (M >= 4).
+// int8 MFMA kernel (M >= 2).
 //
 // The activation rows are the A operand of v_mfma_i32_16x16x32_i8 (rows i) and a
 // 16-row weight tile the B operand (columns n), one 32-weight block per MFMA, so a
@@ -281,8 +281,8 @@ __global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_kernel(int M, const
 
 namespace nve_host {
 
-// The MFMA path serves M >= 4 unless the kernel-selection policy forces one-shot
-// v_dot4 kernels (nve_hip_set_gemv_policy(NVE_GEMV_ONESHOT, ...)).
+// The MFMA path serves M >= 2 (measured faster than v_dot4 from M = 2 on) unless
+// the kernel-selection policy forces one-shot v_dot4 kernels (nve_hip_set_gemv_policy(NVE_GEMV_ONESHOT, ...)).
 static bool batched_use_mfma() { return gemv_policy() != NVE_GEMV_ONESHOT; }
 
 // 16 waves per workgroup (the K quads are dealt round-robin); two 16-row tiles per
@@ -312,7 +312,7 @@ template <int OUT_DT>
 static hipError_t launch_batched_o(int M, const int8_t* xq, const void* xs, int xs_mode,
                                    const uint8_t* nib, const float* ws, void* out, int N, int K,
                                    hipStream_t stream) {
-  if (M >= 4 && batched_use_mfma()) {
+  if (M >= 2 && batched_use_mfma()) {
     if (xs_mode == NVE_XS_ROW_BF16)
       return launch_mfma_m<OUT_DT, NVE_XS_ROW_BF16>(M, xq, xs, nib, ws, out, N, K, stream);
     return launch_mfma_m<OUT_DT, NVE_XS_GROUP32_F32>(M, xq, xs, nib, ws, out, N, K, stream);

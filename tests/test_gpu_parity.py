@@ -451,12 +451,12 @@ def test_dispatch_project(orc, torch_dev, hk, monkeypatch):
     assert rel_err_floor(y16, orc.matvec_w4a16_f64(x, nib, sc, n, k)) <= TOL_W4A16
 
 
-@pytest.mark.parametrize("m", [4, 5, 8, 13, 16])
+@pytest.mark.parametrize("m", [2, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("n,k", [(16, 32), (17, 96), (300, 160), (1000, 2048), (8200, 4096), (70, 14336),
                                  (4096, 14336)])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
-    """M >= 4 runs on the int8 MFMA kernel: ragged N, K with a partial last block quad
+    """M >= 2 runs on the int8 MFMA kernel: ragged N, K with a partial last block quad
     (K % 128 != 0: scalar scale loads), one and two 16-row tiles per workgroup (8200
     rows), every live-element count (M = 4, 5-8, 13-16)."""
     torch = torch_dev
