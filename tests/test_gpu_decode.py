@@ -138,6 +138,30 @@ def test_decode_graph_replay_matches_eager(torch_dev):
     assert int(m.pos.item()) == 40 + n
 
 
+@pytest.mark.parametrize("split", ["2", "4"])
+def test_decode_graph_replay_split_attention(torch_dev, split, monkeypatch):
+    """Key-split attention (partials merged in the o_proj staging) under HIP graph
+    replay: every replayed token and its logits equal the eager sequence bit for bit,
+    with tile counts per split that change as the position crosses tile edges."""
+    torch = torch_dev
+    monkeypatch.setenv("NVE_ATTN_SPLIT", split)
+    m = _model(torch, 4, 2, 64, layers=2, max_seq=1100, prefill=1020)
+    n = 6
+    m.start(3)
+    toks, logits = [], []
+    for _ in range(n):
+        m.step()
+        toks.append(int(m.token.item()))
+        logits.append(m.logits.cpu().numpy().copy())
+    m.start(3)
+    m.capture()
+    for r in range(n):
+        m.generate(1)
+        torch.cuda.synchronize()
+        assert int(m.token.item()) == toks[r], r
+        assert np.array_equal(m.logits.cpu().numpy(), logits[r]), r
+
+
 @pytest.mark.parametrize("fuse", ["1", "0"])
 def test_decode_3b_shape_smoke(torch_dev, fuse, monkeypatch):
     """The Llama-3.2-3B shapes (head_dim 128, GQA 3, ffn 8192, vocab 128256) on 2 layers:
