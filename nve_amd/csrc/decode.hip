@@ -179,8 +179,8 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   __shared__ float s_q[D];
   __shared__ __align__(16) uint16_t s_knew[D];
   __shared__ __align__(16) uint16_t s_vnew[D];
-  __shared__ float s_m[T::NW], s_l[T::NW];
-  __shared__ float s_acc[T::NW * D];
+  __shared__ float s_m[T::NW], s_l[T::NW], s_f[T::NW], s_ml[2];
+  __shared__ __align__(16) float s_acc[T::NW * D];
 
   const int G = num_heads / num_kv_heads;
   // Workgroups are dealt to the 8 XCDs round-robin (XCD = block % 8), each with its own
@@ -203,9 +203,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   const size_t cache_base = (size_t)kvh * max_seq * D;
 
   // three tile buffers in a ring; the first three tiles' loads are issued at once (their
-  // addresses do not depend on the position).  Loads are unconditional (tile indices
-  // past the end re-read the last tile) so the compiler's wait for one buffer never
-  // covers a younger one.
+  // addresses do not depend on the position, rows past the end are masked at use)
   AttnTile<D> b0, b1, b2;
   attn_issue<D>(b0, kc, vc, cache_base, sp, max_seq, wave, krow, col);
   attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, max_seq, wave, krow, col);
@@ -227,7 +225,6 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   const int ntiles = (len + T::KT - 1) / T::KT;
   // this workgroup's tiles: sp + SPLIT * j for j < nt
   const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
-  const int last = nt - 1;
 
   if (tid < HALF) {
     const float c = rope_cos[(size_t)pos * HALF + tid], sn = rope_sin[(size_t)pos * HALF + tid];
@@ -251,17 +248,19 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   float m_run = -INFINITY, l_run = 0.0f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  // a buffer is refilled only when a later tile of this workgroup remains: loads past
+  // the last tile would only be waited for (their registers are reused by the merge)
   for (int j = 0; j < nt; j += 3) {
     attn_compute<D>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
-    attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * min(j + 3, last), len, wave, krow, col);
+    if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
     if (j + 1 < nt)
       attn_compute<D>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run,
                       acc);
-    attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * min(j + 4, last), len, wave, krow, col);
+    if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
     if (j + 2 < nt)
       attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run,
                       acc);
-    attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * min(j + 5, last), len, wave, krow, col);
+    if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
   }
   // merge the rows of the wave (same columns), then the waves through LDS
   l_run = stride_sum<T::LPK>(l_run);
@@ -276,17 +275,34 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     }
   }
   lds_barrier();
-  if (tid < D / 4) {
+  // wave weights e^(m_w - M) once (lanes 0..15 of wave 0), then every output column
+  // is a plain weighted sum of the 16 wave accumulators
+  if (tid < T::NW) {
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < T::NW; ++w) M = fmaxf(M, s_m[w]);
-    float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float f = s_m[tid] == -INFINITY ? 0.0f : expf(s_m[tid] - M);
+    s_f[tid] = f;
+    if (tid == 0) {
+      float L = 0.0f;
+#pragma unroll
+      for (int w = 0; w < T::NW; ++w) L = fmaf(s_m[w] == -INFINITY ? 0.0f : expf(s_m[w] - M), s_l[w], L);
+      s_ml[0] = M;
+      s_ml[1] = L;
+    }
+  }
+  lds_barrier();
+  if (tid < D / 4) {
+    const float M = s_ml[0], L = s_ml[1];
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int w = 0; w < T::NW; ++w) {
-      const float f = s_m[w] == -INFINITY ? 0.0f : expf(s_m[w] - M);
-      L = fmaf(f, s_l[w], L);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = fmaf(f, s_acc[w * D + 4 * tid + e], o[e]);
+      const float f = s_f[w];
+      const float4 a4 = *(const float4*)&s_acc[w * D + 4 * tid];
+      o[0] = fmaf(f, a4.x, o[0]);
+      o[1] = fmaf(f, a4.y, o[1]);
+      o[2] = fmaf(f, a4.z, o[2]);
+      o[3] = fmaf(f, a4.w, o[3]);
     }
     if (OUT == 3) {
       float* rec = out_part + ((size_t)sp * num_heads + hq) * (D + 4);
