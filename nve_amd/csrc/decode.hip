@@ -567,7 +567,7 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
                                    bool w4a8, int split, hipStream_t s) {
   const float scale = 1.0f / sqrtf((float)c.head_dim);
   // (kv head, split) pairs a multiple of 8: each XCD gets whole groups of query heads
-  const int xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1 && !getenv("NVE_ATTN_NOXCD");
+  const int xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1;
 #define NVE_ATTN(D, OUT, S)                                                                                     \
   hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
                      ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,             \
