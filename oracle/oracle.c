@@ -37,6 +37,8 @@
  *   orc_q4_matvec_f32       equals row-wise orc_q4_dot_row_* for every row and
  *                           thread count (row split must not change results).
  *   orc_quantize_q8_group   KATs: +-amax -> +-127, RNE ties (2.5 -> 2, 3.5 -> 4),
+ *                           NaN / Inf groups (the fmaxf tree drops NaN, NaN codes
+ *                           are 0, an infinite amax zeroes the group),
  *                           all-zero group -> scale 1, q 0; brute force with numpy
  *                           float32 ops.
  *   orc_quantize_q8_rows_bf16 same KAT family with a bf16 scale.

@@ -84,6 +84,20 @@ def test_quantize_q8_kat_ties_and_zero_group(orc, torch_dev, hk):
     assert np.all(down(xq)[32:] == 0) and np.all(down(xs) == 1.0)
 
 
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+def test_quantize_q8_nonfinite(orc, torch_dev, hk, xdt):
+    """NaN / +-Inf activations: the same codes and scales as the reference kernel's
+    semantics restated in the oracle (NaN ignored by the max, scale inf -> codes 0)."""
+    torch = torch_dev
+    from test_oracle import _nonfinite_groups
+    x = _nonfinite_groups()
+    xt = up(torch, x.astype(np.float16)) if xdt == "f16" else up(torch, x)
+    xq, xs = hk.quantize_f16_q8(xt)
+    q_ref, s_ref = orc.quantize_q8_group(x)
+    assert np.array_equal(down(xq), q_ref)
+    assert np.array_equal(down(xs).view(np.uint32), s_ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("m,k", [(1, 2048), (4, 4096), (16, 14336), (3, 96)])
 def test_quantize_q8_rows_exact(orc, torch_dev, hk, m, k):
     torch = torch_dev
@@ -499,6 +513,28 @@ def test_w4a8_fused_quantize_bit_identical(orc, torch_dev, hk, n, k, xdt, odt):
                        y2.view(torch.int16 if odt == "f16" else torch.int32))
     xq_ref, _ = orc.quantize_q8_group(down(xt.float()))
     assert np.array_equal(down(xq), xq_ref)
+
+
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+def test_w4a8_fused_quantize_nonfinite(orc, torch_dev, hk, xdt):
+    """NaN / +-Inf activations through the fused quantize + GEMV: bit-identical to the
+    two-launch sequence (the infinite-scale groups make their outputs NaN in both)."""
+    torch = torch_dev
+    from test_oracle import _nonfinite_groups
+    n, k = 96, 256
+    _, _, nib, ws = _problem(orc, n, k, seed=5)
+    x = np.tile(_nonfinite_groups(), 2)
+    x[128:] = np.where(np.isfinite(x[128:]), x[128:], 0.5)  # second half finite
+    xt = up(torch, x.astype(np.float16)) if xdt == "f16" else up(torch, x)
+    tn, tw = up(torch, nib), up(torch, ws)
+    y1 = hk.matvec_w4a8_x(xt, tn, tw, n, k, out_dtype=torch.float32)
+    xq, xs = hk.quantize_f16_q8(xt)
+    y2 = torch.empty(n, dtype=torch.float32, device="cuda")
+    hk.matvec_w4a8_into(xq, xs, tn, tw, y2, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    q_ref, s_ref = orc.quantize_q8_group(down(xt.float()))
+    assert np.array_equal(down(xq), q_ref) and np.array_equal(down(xs).view(np.uint32), s_ref.view(np.uint32))
 
 
 def test_w4a8_fused_quantize_grouped(orc, torch_dev, hk):

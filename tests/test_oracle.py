@@ -268,6 +268,28 @@ def test_q8_group_kat(orc):
     assert np.all(xq[32:] == 0)
 
 
+def _nonfinite_groups():
+    x = np.zeros(128, F32)
+    x[0], x[1], x[2] = np.nan, 3.0, -1.5   # NaN dropped by fmaxf: amax 3
+    x[32], x[33] = np.inf, 1.0             # amax inf: scale inf, 1/scale 0
+    x[64:96] = np.nan                      # all NaN: amax not > 0 -> scale 1
+    x[96], x[97] = -np.inf, -2.0
+    return x
+
+
+def test_q8_group_kat_nonfinite(orc):
+    """cuda/nve_kernels.cu:712-745 on NaN / Inf: the fmaxf tree ignores NaN, a group
+    whose amax is not > 0 keeps scale 1, __float2int_rn(NaN) is 0, and an infinite
+    amax gives scale inf, 1/scale = 0, so every code of that group is 0 (inf * 0 is
+    NaN -> 0)."""
+    xq, sc = orc.quantize_q8_group(_nonfinite_groups())
+    assert sc[0] == F32(3.0) / F32(127.0)
+    assert list(xq[:3]) == [0, 127, -64]   # -1.5 * 127 / 3 = -63.5 -> -64 (RNE)
+    assert np.isposinf(sc[1]) and np.all(xq[32:64] == 0)
+    assert sc[2] == 1.0 and np.all(xq[64:96] == 0)
+    assert np.isposinf(sc[3]) and np.all(xq[96:128] == 0)
+
+
 def test_q8_group_brute_force(orc):
     x = activations(4096, seed=21)
     xq, sc = orc.quantize_q8_group(x)
