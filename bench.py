@@ -465,8 +465,9 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool) -> d
 
 def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     """The prefill-adjacency row: W4A16 GEMM X[M, K] @ W^T at the 8B gate shape
-    (14336 x 4096), fp16 activations, fp32 output, M in {16, 128, 512, 2048}: the fused
-    MFMA kernel (nve_hip_gemm_w4a16) against the reference's own method on the same GPU
+    (14336 x 4096), fp16 activations, fp32 output, M in {1, 4, 16, 128, 512, 2048}: the
+    fused MFMA kernels of nve_hip_gemm_w4a16 (weight-streaming for M <= 16, tiled above)
+    against the reference's own method on the same GPU
     (nve_dequant_w4a16 to fp16, then a dense fp16 GEMM -- torch.matmul, i.e. the
     vendor BLAS -- as GpuWeight::matmul_x does with candle, src/gpu_layer.rs:219-237).
     Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time."""
@@ -474,7 +475,7 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     n, k = 14336, 4096
     nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
     out = {"shape": f"{n}x{k}", "x_dtype": "f16", "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS, "rows": []}
-    for m in (16, 128, 512, 2048):
+    for m in (1, 4, 16, 128, 512, 2048):
         x = torch.randn((m, k), generator=g, device="cuda").half()
         wf = hk.dequant_w4(nib, sc, n, k)
 

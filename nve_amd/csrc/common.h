@@ -114,6 +114,32 @@ __device__ __forceinline__ float stride_max(float v) {
   return xor32_partner_max(v);
 }
 
+// 4x4 transpose between the four 16-lane groups and four registers: (lane group g,
+// register c) -> (lane group c, register g), via two permlane32 and two permlane16 swaps.
+__device__ __forceinline__ void transpose4(uint32_t& c0, uint32_t& c1, uint32_t& c2, uint32_t& c3) {
+  auto s02 = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
+  c0 = s02[0];
+  c2 = s02[1];
+  c1 = s13[0];
+  c3 = s13[1];
+  auto s01 = __builtin_amdgcn_permlane16_swap(c0, c1, false, false);
+  auto s23 = __builtin_amdgcn_permlane16_swap(c2, c3, false, false);
+  c0 = s01[0];
+  c1 = s01[1];
+  c2 = s23[0];
+  c3 = s23[1];
+}
+
+// Value of v in lane src_lane (ds_bpermute: through the LDS crossbar, no LDS storage).
+__device__ __forceinline__ uint32_t lane_fetch(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+__device__ __forceinline__ uint4 lane_fetch4(uint4 v, int src_lane) {
+  return make_uint4(lane_fetch(v.x, src_lane), lane_fetch(v.y, src_lane), lane_fetch(v.z, src_lane),
+                    lane_fetch(v.w, src_lane));
+}
+
 // Pairs of lanes (2i, 2i+1).
 __device__ __forceinline__ int pair_sum_i(int v) { return v + dpp_mov_i<0xB1>(v); }
 

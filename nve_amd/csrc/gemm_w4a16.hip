@@ -14,9 +14,11 @@
 // 2 x 2 MFMA tiles of 32 x 32 (v_mfma_f32_32x32x16: half the LDS operand traffic per
 // flop of 16 x 16 tiles); K advances 64 per slice (two Q4 blocks).  The global
 // loads (X rows, nibbles, scales) run two slices ahead of the MFMAs and the LDS is
-// double-buffered, so the dequantization of slice t+1 overlaps the MFMAs of slice t, so HBM latency overlaps the
-// math; small-M launches also split K over workgroups (fp32 atomic accumulation).  LDS rows are padded
-// (72 elements) so the ds_read_b128 of a fragment spreads over the banks.
+// double-buffered, so the dequantization of slice t+1 overlaps the MFMAs of slice t and
+// HBM latency overlaps the math; launches with few output tiles also split K over
+// workgroups (fp32 atomic accumulation).  LDS rows are padded (72 elements) so the
+// ds_read_b128 of a fragment spreads over the banks.  M <= 16 runs a separate
+// weight-streaming kernel (gemm_w4a16_small_kernel below).
 
 #include "common.h"
 #include "w4_launch.h"
@@ -203,6 +205,176 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
 }
 
+// ---- small M (M <= 16): weight-streaming form ---------------------------------
+// For a few activation rows the tile GEMM above re-dequantizes little and streams
+// less: this kernel is the batched-GEMV layout of the W4A8 MFMA kernel with a fp16 /
+// bf16 MFMA (v_mfma_f32_16x16x32_{f16,bf16}).  The activation rows are the A operand
+// (rows i; activation row m sits in A row 4 (m % 4) + m / 4), a 16-row weight tile
+// the B operand; lane group g of a block takes the k-set {4g..4g+3} u {16+4g..16+4g+3}
+// -- the low and high nibbles of nibble dword g -- in A and B alike.  The B operand is
+// the reference dequant, rounded exactly as nve_dequant_w4a16 rounds it:
+// fma(n, s, -8 s) (= the f32 product (n - 8) s) [* awq], materialised as f32, then RNE
+// to fp16 / bf16 (v_cvt_pk_{f16,bf16}_f32); the fp32 MFMA accumulator runs over all of
+// K, so there is no per-block epilogue.  Loads are issued row-major (4 consecutive
+// lanes on 64 contiguous bytes of one row) and moved to the operand lanes with
+// ds_bpermute and the 4x4 lane-group transpose; a workgroup owns T tiles and its 16
+// waves deal the K quads (4 blocks) round-robin.
+template <bool BF16, bool AWQ, int T>
+struct SmallQuad {
+  uint2 xl[4], xh[4];  // block 4q+j of activation row r: elements 4p..4p+3, 16+4p..16+4p+3
+  uint4 w[T];          // block 4q+p of weight row r
+  float4 sc[T];        // scales of the quad's 4 blocks, weight row r
+  float4 al[AWQ ? 4 : 1], ah[AWQ ? 4 : 1];  // awq at the lane's k-set of each block
+};
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+  // the f32 values are materialised first: a fused multiply-convert would round the
+  // exact product once instead of rounding the f32 product
+  asm volatile("" : "+v"(a), "+v"(b));
+  if (BF16) {
+    typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+    const bf2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  const half2_t v = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <bool BF16, bool AWQ, int T>
+__device__ __forceinline__ void small_issue(SmallQuad<BF16, AWQ, T>& st, const uint2* xrow, const float* awq,
+                                            const uint4* const (&wrow)[T], const float* const (&srow)[T],
+                                            int vec_sc, int q, int nb, int g, int lp) {
+  // activations (block 4q+j: 8-byte pieces p and 4+p of the 64-byte block row), weights
+  // and scales (clamped to the last block: weighted 0 at use)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = min(4 * q + j, nb - 1);
+    st.xl[j] = xrow[8 * b + lp];
+    st.xh[j] = xrow[8 * b + 4 + lp];
+    if (AWQ) {
+      st.al[j] = *(const float4*)(awq + 32 * b + 4 * g);
+      st.ah[j] = *(const float4*)(awq + 32 * b + 16 + 4 * g);
+    }
+  }
+  const int bl = min(4 * q + lp, nb - 1);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    st.w[t] = ld_stream(wrow[t] + bl);
+    if (vec_sc) {
+      st.sc[t] = ((const float4*)srow[t])[q];
+    } else {
+      st.sc[t].x = srow[t][min(4 * q + 0, nb - 1)];
+      st.sc[t].y = srow[t][min(4 * q + 1, nb - 1)];
+      st.sc[t].z = srow[t][min(4 * q + 2, nb - 1)];
+      st.sc[t].w = srow[t][min(4 * q + 3, nb - 1)];
+    }
+  }
+}
+
+template <bool BF16, bool AWQ, int T>
+__device__ __forceinline__ void small_compute(const SmallQuad<BF16, AWQ, T>& st, int q, int nb, bool m_ok, int src_w,
+                                              int src_x, f4_t (&acc)[T]) {
+  // A operands: lane (i, g) <- load lane (m(i), g)
+  uint4 a[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t d0 = lane_fetch(st.xl[j].x, src_x), d1 = lane_fetch(st.xl[j].y, src_x);
+    const uint32_t d2 = lane_fetch(st.xh[j].x, src_x), d3 = lane_fetch(st.xh[j].y, src_x);
+    a[j] = m_ok ? make_uint4(d0, d1, d2, d3) : make_uint4(0, 0, 0, 0);
+  }
+  const bool full = 4 * q + 3 < nb;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint4 w = lane_fetch4(st.w[t], src_w);
+    uint32_t c0 = w.x, c1 = w.y, c2 = w.z, c3 = w.w;
+    transpose4(c0, c1, c2, c3);  // lane (n, g): nibble dword g of blocks 4q+0..3
+    const uint32_t cj[4] = {c0, c1, c2, c3};
+    const uint4 sw = lane_fetch4(make_uint4(__float_as_uint(st.sc[t].x), __float_as_uint(st.sc[t].y),
+                                            __float_as_uint(st.sc[t].z), __float_as_uint(st.sc[t].w)),
+                                 src_w);
+    const float scj[4] = {__uint_as_float(sw.x), __uint_as_float(sw.y), __uint_as_float(sw.z),
+                          __uint_as_float(sw.w)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s = scj[j], s8 = -8.0f * s;
+      const uint32_t lo = cj[j] & 0x0F0F0F0Fu, hi = (cj[j] >> 4) & 0x0F0F0F0Fu;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = fmaf((float)((lo >> (8 * e)) & 0xffu), s, s8);
+        v[4 + e] = fmaf((float)((hi >> (8 * e)) & 0xffu), s, s8);
+      }
+      if (AWQ) {
+        const float al[4] = {st.al[j].x, st.al[j].y, st.al[j].z, st.al[j].w};
+        const float ah[4] = {st.ah[j].x, st.ah[j].y, st.ah[j].z, st.ah[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] *= al[e];
+          v[4 + e] *= ah[e];
+        }
+      }
+      uint4 b = make_uint4(cvt_pk<BF16>(v[0], v[1]), cvt_pk<BF16>(v[2], v[3]), cvt_pk<BF16>(v[4], v[5]),
+                           cvt_pk<BF16>(v[6], v[7]));
+      // blocks past the end (last quad only) were loaded clamped: multiply zeros
+      if (!(full || 4 * q + j < nb)) b = make_uint4(0, 0, 0, 0);
+      acc[t] = mfma16<BF16>(a[j], b, acc[t]);
+    }
+  }
+}
+
+template <bool BF16, bool AWQ, int OUT_DT, int KS, int T>
+__global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_t* __restrict__ x,
+                                                                   const uint8_t* __restrict__ nib,
+                                                                   const float* __restrict__ ws,
+                                                                   const float* __restrict__ awq,
+                                                                   void* __restrict__ out, int M, int N, int K,
+                                                                   int vec_sc) {
+  __shared__ float s_red[KS][T * 16][17];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;  // operand layout
+  const int lr = lane >> 2, lp = lane & 3;  // load layout
+  const int row0 = blockIdx.x * (16 * T);
+  const int nb = K >> 5;
+  const int nq = (nb + 3) >> 2;
+  const size_t row_bytes = (size_t)(K >> 1);
+  const uint4* wrow[T];
+  const float* srow[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int r = min(row0 + 16 * t + lr, N - 1);
+    wrow[t] = (const uint4*)(nib + (size_t)r * row_bytes);
+    srow[t] = ws + (size_t)r * nb;
+  }
+  const uint2* xrow = (const uint2*)(x + (size_t)min(lr, M - 1) * K);  // 8-byte units
+  const int am = 4 * (nl & 3) + (nl >> 2);
+  const bool m_ok = am < M;
+  const int src_w = 4 * nl + g, src_x = 4 * am + g;
+  f4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int q = wave; q < nq; q += KS) {
+    SmallQuad<BF16, AWQ, T> st;
+    small_issue<BF16, AWQ, T>(st, xrow, awq, wrow, srow, vec_sc, q, nb, g, lp);
+    small_compute<BF16, AWQ, T>(st, q, nb, m_ok, src_w, src_x, acc);
+  }
+  // D layout: lane (n, g) holds rows i = 4g + e (activation row 4e + g) of column n
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_red[wave][16 * t + nl][4 * e + g] = acc[t][e];
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * 16 * 16; i += 64 * KS) {
+    const int mm = i / (16 * T), r = i % (16 * T);
+    float y = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < KS; ++w2) y += s_red[w2][r][mm];
+    if (mm < M && row0 + r < N) store_out<OUT_DT>(out, (size_t)mm * N + row0 + r, y);
+  }
+}
+
 __global__ __launch_bounds__(256) void zero_f32_kernel(float4* __restrict__ p, size_t n4) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n4) p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -214,6 +386,9 @@ __global__ __launch_bounds__(256) void zero_f32_kernel(float4* __restrict__ p, s
 }  // namespace nve
 
 namespace nve_host {
+
+constexpr int kGemmSmallM = 16;
+constexpr int kSmallKS = 16;
 
 template <bool BF16, bool AWQ>
 static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
@@ -251,9 +426,40 @@ static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const 
   return hipGetLastError();
 }
 
+// M <= 16: the weight-streaming kernel (two 16-row tiles per workgroup while that
+// leaves at least 256 workgroups, else one; 16 waves per workgroup).
+template <bool BF16, bool AWQ, int OUT_DT>
+static hipError_t launch_small_o(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                                 void* out, int N, int K, hipStream_t s) {
+  const int vec_sc = (K % 128 == 0) && aligned(sc, 16);
+  if ((N + 31) / 32 >= 256)
+    hipLaunchKernelGGL((nve::gemm_w4a16_small_kernel<BF16, AWQ, OUT_DT, kSmallKS, 2>), dim3((N + 31) / 32),
+                       dim3(64 * kSmallKS), 0, s, (const uint16_t*)x, nib, sc, awq, out, M, N, K, vec_sc);
+  else
+    hipLaunchKernelGGL((nve::gemm_w4a16_small_kernel<BF16, AWQ, OUT_DT, kSmallKS, 1>), dim3((N + 15) / 16),
+                       dim3(64 * kSmallKS), 0, s, (const uint16_t*)x, nib, sc, awq, out, M, N, K, vec_sc);
+  return hipGetLastError();
+}
+
+template <bool BF16, bool AWQ>
+static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                               void* out, int out_dt, int N, int K, hipStream_t s) {
+  switch (out_dt) {
+    case NVE_DT_F16: return launch_small_o<BF16, AWQ, NVE_DT_F16>(x, M, nib, sc, awq, out, N, K, s);
+    case NVE_DT_BF16: return launch_small_o<BF16, AWQ, NVE_DT_BF16>(x, M, nib, sc, awq, out, N, K, s);
+    default: return launch_small_o<BF16, AWQ, NVE_DT_F32>(x, M, nib, sc, awq, out, N, K, s);
+  }
+}
+
 hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, const float* awq,
                              void* out, int out_dt, int N, int K, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
+  if (M <= kGemmSmallM) {
+    if (awq) return bf ? launch_small<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, s)
+                       : launch_small<false, true>(x, M, nib, sc, awq, out, out_dt, N, K, s);
+    return bf ? launch_small<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, s)
+              : launch_small<false, false>(x, M, nib, sc, awq, out, out_dt, N, K, s);
+  }
   if (awq) return bf ? launch_gemm_t<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, s)
                      : launch_gemm_t<false, true>(x, M, nib, sc, awq, out, out_dt, N, K, s);
   return bf ? launch_gemm_t<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, s)

@@ -105,30 +105,6 @@ __global__ __launch_bounds__(256) void w4a8_batched_dot4_kernel(int M, const int
 // wave + KS, ... of K and meet in LDS.
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void transpose4(uint32_t& c0, uint32_t& c1, uint32_t& c2, uint32_t& c3) {
-  // (lane group g, register c) -> (lane group c, register g)
-  auto s02 = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
-  auto s13 = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
-  c0 = s02[0];
-  c2 = s02[1];
-  c1 = s13[0];
-  c3 = s13[1];
-  auto s01 = __builtin_amdgcn_permlane16_swap(c0, c1, false, false);
-  auto s23 = __builtin_amdgcn_permlane16_swap(c2, c3, false, false);
-  c0 = s01[0];
-  c1 = s01[1];
-  c2 = s23[0];
-  c3 = s23[1];
-}
-
-__device__ __forceinline__ uint32_t lane_fetch(uint32_t v, int src_lane) {
-  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
-}
-__device__ __forceinline__ uint4 lane_fetch4(uint4 v, int src_lane) {
-  return make_uint4(lane_fetch(v.x, src_lane), lane_fetch(v.y, src_lane), lane_fetch(v.z, src_lane),
-                    lane_fetch(v.w, src_lane));
-}
-
 // One quad of K: activations (two 16-byte halves of block 4q+p of activation row r)
 // and, per tile, weights (block 4q+p of weight row r) and the quad's 4 weight scales,
 // all in the row-major load layout.

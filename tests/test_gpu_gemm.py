@@ -40,7 +40,8 @@ def _round(a, dt):
     return a.astype(np.float16).astype(np.float32) if dt == "f16" else to_bf16(a)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (2, 1000, 4096), (16, 200, 192), (16, 8200, 1024),
+                                   (17, 96, 1024), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_parity(orc, torch_dev, hk, m, n, k, xdt, with_awq):
@@ -81,10 +82,36 @@ def test_gemm_w4a16_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_
     assert np.array_equal(y.cpu().numpy().T.view(np.uint32), wref.view(np.uint32))
 
 
-@pytest.mark.parametrize("odt,tol", [("bf16", 2.0 ** -8 + 2e-3), ("f16", 2.0 ** -11 + 2e-3)])
-def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol):
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("with_awq", [False, True])
+def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_awq):
+    """M <= 16 runs the weight-streaming kernel: 16 rows of the identity at a time
+    (X = I[k0 : k0 + 16]) read back 16 columns of the weight matrix as the kernel
+    rounded it, which must equal the reference dequant bit for bit; K = 448 leaves a
+    partial last quad of blocks."""
     torch = torch_dev
-    m, n, k = 33, 192, 2048
+    n, k = 70, 448
+    data = orc.q4_from_f32(weights(n, k, seed=41, std=0.3))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    awq = np.random.default_rng(42).uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
+    wref = _round(orc.q4_to_f32(data, n, k, awq), xdt)
+    tdt = torch.float16 if xdt == "f16" else torch.bfloat16
+    eye = torch.eye(k, dtype=tdt, device="cuda")
+    tn, ts = torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda()
+    ta = None if awq is None else torch.from_numpy(awq).cuda()
+    got = np.zeros((k, n), np.float32)
+    for k0 in range(0, k, 16):
+        y = hk.gemm_w4a16(eye[k0:k0 + 16].contiguous(), tn, ts, n, k, ta, out_dtype=torch.float32)
+        got[k0:k0 + 16] = y.cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.array_equal(got.T.view(np.uint32), wref.view(np.uint32))
+
+
+@pytest.mark.parametrize("odt,tol", [("bf16", 2.0 ** -8 + 2e-3), ("f16", 2.0 ** -11 + 2e-3)])
+@pytest.mark.parametrize("m", [33, 5])
+def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
+    torch = torch_dev
+    n, k = 192, 2048
     rng = np.random.default_rng(5)
     data = orc.q4_from_f32(weights(n, k, seed=9, std=0.05))
     nib, sc = orc.extract_for_gpu(data, n, k)
