@@ -41,7 +41,7 @@ def _round(a, dt):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (2, 1000, 4096), (16, 200, 192), (16, 8200, 1024),
-                                   (17, 96, 1024), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
+                                   (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_parity(orc, torch_dev, hk, m, n, k, xdt, with_awq):
