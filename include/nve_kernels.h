@@ -282,10 +282,10 @@ typedef struct nve_decode_io {
   const int *pos;         /* device int: position of this token (< max_seq) */
   const float *rope_cos;  /* f32 [max_seq, D/2] */
   const float *rope_sin;  /* f32 [max_seq, D/2] */
-  void *workspace;        /* nve_hip_decode_workspace_bytes() bytes, 256-byte aligned,
-                             zero-filled once after allocation (it holds arrival
-                             counters that every call leaves at zero); one workspace
-                             per stream: calls sharing one must not overlap */
+  void *workspace;        /* nve_hip_decode_workspace_bytes() bytes, 256-byte aligned
+                             (scratch: every call writes what it reads, no
+                             initialisation needed); one workspace per stream:
+                             calls sharing one must not overlap */
 } nve_decode_io;
 
 typedef struct nve_decode_head {

@@ -19,15 +19,6 @@
 
 namespace nve {
 
-// Loads that must see other workgroups' stores from the same launch (after their
-// release fence): device-scope atomic loads bypass the CU's vector L1.
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_agent(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // ---- RMSNorm ------------------------------------------------------------------
 // y_i = h_i * w_i / sqrt(mean(h^2) + eps): sum of squares and the scaling in f64 as
 // src/ops.rs:12-30, output rounded once.  One workgroup of 1024 threads; thread t
@@ -349,9 +340,10 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
 }
 
 // ---- head: greedy argmax (first maximum), next-token embedding, position advance --
-// grid kArgmaxBlocks x 256: each workgroup reduces a slice of the logits to (value,
-// index); the last to arrive (device-scope counter, reset by it) reduces the partials,
-// writes the token, embeds its row into hidden and advances the position.  NaN never
+// Two launches: kArgmaxBlocks workgroups each reduce a slice of the logits to (value,
+// index); one workgroup then reduces the partials, writes the token, embeds its row
+// into hidden and advances the position (the launch boundary orders the partials'
+// writes before their reads -- no device-scope fence or arrival counter).  NaN never
 // wins; among equal values the lowest index wins (src/ops.rs:485-495 keeps the first
 // maximum).
 constexpr int kArgmaxBlocks = 128;
@@ -374,18 +366,12 @@ __device__ __forceinline__ void argmax_block(float& best, int& bi, float* s_v, i
     for (int w = 1; w < 4; ++w) argmax_merge(best, bi, s_v[w], s_i[w]);
 }
 
-__global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restrict__ logits, int V,
-                                                           const uint16_t* __restrict__ embed, int H,
-                                                           float* __restrict__ hidden, int* __restrict__ token_out,
-                                                           int* __restrict__ d_pos, float* __restrict__ part_v,
-                                                           int* __restrict__ part_i, int* __restrict__ counter) {
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits, int V,
+                                                             float* __restrict__ part_v, int* __restrict__ part_i) {
   __shared__ float s_v[4];
   __shared__ int s_i[4];
-  __shared__ int s_last;
-  __shared__ int s_tok;
   // slices of a multiple of 1024 logits: every thread reads whole float4s, four of
-  // them issued before any is compared (the logits come from another XCD's writes,
-  // so each round trip is a full memory latency)
+  // them issued before any is compared
   const int per = ((V + kArgmaxBlocks - 1) / kArgmaxBlocks + 1023) & ~1023;
   const int lo = blockIdx.x * per, hi = min(V, lo + per);
   float best = -INFINITY;
@@ -419,25 +405,28 @@ __global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restri
   if (threadIdx.x == 0) {
     part_v[blockIdx.x] = best;
     part_i[blockIdx.x] = bi;
-    __threadfence();
-    s_last = atomicAdd(counter, 1) == kArgmaxBlocks - 1;
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  best = -INFINITY;
-  bi = 0x7fffffff;
+}
+
+__global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restrict__ part_v,
+                                                           const int* __restrict__ part_i,
+                                                           const uint16_t* __restrict__ embed, int H,
+                                                           float* __restrict__ hidden, int* __restrict__ token_out,
+                                                           int* __restrict__ d_pos) {
+  __shared__ float s_v[4];
+  __shared__ int s_i[4];
+  __shared__ int s_tok;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
   if (threadIdx.x < kArgmaxBlocks) {
-    best = ld_agent(part_v + threadIdx.x);
-    bi = ld_agent(part_i + threadIdx.x);
+    best = part_v[threadIdx.x];
+    bi = part_i[threadIdx.x];
   }
-  __syncthreads();  // s_v / s_i reuse
   argmax_block(best, bi, s_v, s_i);
   if (threadIdx.x == 0) {
     if (bi == 0x7fffffff) bi = 0;  // all NaN / -inf: token 0
     s_tok = bi;
     *token_out = bi;
-    atomicExch(counter, 0);
   }
   __syncthreads();
   const int tok = s_tok;
@@ -459,7 +448,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
 namespace nve_host {
 
 struct DecodeWs {
-  int* counters;       // [1] argmax arrival counter (zero at rest)
   uint16_t* act_bf16;  // [max(H, Hq*D, F)]
   int8_t* xq;          // [max(H, Hq*D, F)]
   float* xs;           // [max/32]
@@ -492,7 +480,6 @@ static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
     off += align256(bytes);
     return r;
   };
-  w.counters = (int*)take(4);
   w.act_bf16 = (uint16_t*)take(mx * 2);
   w.xq = (int8_t*)take(mx);
   w.xs = (float*)take(mx / 32 * 4);
@@ -691,9 +678,10 @@ int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8
     NVE_TRY(launch_rmsnorm(c, hd.hidden, hd.final_norm, w4a8, ws, s));
     NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
   }
-  hipLaunchKernelGGL(nve::argmax_embed_kernel, dim3(nve::kArgmaxBlocks), dim3(256), 0, s, logits, hd.lm_head.n,
-                     hd.embed, c.hidden, hd.hidden, hd.token_out, hd.pos, ws.arg_v, ws.arg_i,
-                     ws.counters);
+  hipLaunchKernelGGL(nve::argmax_partial_kernel, dim3(nve::kArgmaxBlocks), dim3(256), 0, s, logits, hd.lm_head.n,
+                     ws.arg_v, ws.arg_i);
+  hipLaunchKernelGGL(nve::argmax_embed_kernel, dim3(1), dim3(256), 0, s, ws.arg_v, ws.arg_i, hd.embed, c.hidden,
+                     hd.hidden, hd.token_out, hd.pos);
   return (int)hipGetLastError();
 }
 

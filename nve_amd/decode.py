@@ -131,7 +131,7 @@ class DecodeModel:
 
         self.cfg = DecodeConfig(H, s.heads, s.kv_heads, D, F, max_seq, s.vocab, s.eps)
         ws_bytes = int(L.nve_hip_decode_workspace_bytes(C.byref(self.cfg)))
-        self.workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)  # counters start at 0
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)  # scratch
         self.hidden = torch.zeros(H, dtype=torch.float32, device=device)
         self.pos = torch.full((1,), prefill, dtype=torch.int32, device=device)
         self.token = torch.zeros(1, dtype=torch.int32, device=device)
