@@ -506,6 +506,19 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     return out
 
 
+def decode_traffic_probe(torch) -> None:
+    """Six eager 3B decode steps (the bench's model: max_seq 1024, 512 prefilled
+    positions) for per-dispatch HBM counters; eager launches because counter collection
+    over HIP-graph replays crashed the profiler's host library."""
+    from nve_amd.decode import LLAMA_3_2_3B, DecodeModel
+    m = DecodeModel(LLAMA_3_2_3B, max_seq=1024, prefill=512)
+    m.start(1)
+    for _ in range(6):
+        m.step()
+    torch.cuda.synchronize()
+    log(f"decode traffic probe: 6 steps, algorithmic bytes per step {m.step_bytes()}")
+
+
 def traffic_probe(torch, L, hk):
     """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
     256 MiB (calibration: 256 MiB read + 256 MiB written), then 5 launches of the
@@ -552,6 +565,8 @@ def main():
                     help="run only the 3B decode measurement (for profiling; no bench line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no bench line)")
+    ap.add_argument("--decode-traffic-probe", action="store_true",
+                    help="6 eager (not graph-replayed) 3B decode steps for rocprofv3 --pmc (no bench line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -566,6 +581,9 @@ def main():
     torch.cuda.set_device(0)
     if args.traffic_probe:
         traffic_probe(torch, L, hk)
+        return
+    if args.decode_traffic_probe:
+        decode_traffic_probe(torch)
         return
     if args.decode_only:
         print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True)}))
