@@ -19,8 +19,9 @@
 //             own activations: nve_quantize_f16_q8 + nve_matvec_w4a8 in one launch).
 //   SRC_ATTN2 / SRC_ATTN4: the decode attention output, merged from the partials of 2
 //             or 4 key splits: a = records [split][head] of (m, l, -, -, acc[D]) with
-//             m the running max, l the sum of e^(s - m), acc the unnormalised value
-//             sum; x = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s (M = max_s m_s);
+//             m the running max of the scores in log2 units (q . k * log2(e) / sqrt(D)),
+//             l the sum of 2^(s - m), acc the unnormalised value sum;
+//             x = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s (M = max_s m_s);
 //             i0 = head_dim, i1 = num_heads.
 #pragma once
 
@@ -117,7 +118,7 @@ __device__ __forceinline__ void prod_values(const ProdChunk<SRC, E>& c, double i
     float f[S], L = 0.0f;
 #pragma unroll
     for (int sp = 0; sp < S; ++sp) {
-      f[sp] = c.ml[sp].x == -INFINITY ? 0.0f : expf(c.ml[sp].x - M);
+      f[sp] = c.ml[sp].x == -INFINITY ? 0.0f : exp2f(c.ml[sp].x - M);
       L = fmaf(f[sp], c.ml[sp].y, L);
     }
     const float invL = 1.0f / L;

@@ -74,10 +74,12 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 // are spread over the waves in tiles: a key's row of D bf16 (D/8 16-byte pieces)
 // sits in LPK = D/8 consecutive lanes, one piece per lane, so the q.k dot product is
 // a butterfly over those lanes and the value sum accumulates each lane's 8 columns.
-// Every wave keeps its own online softmax (running max m, sum l, accumulator
-// rescaled by e^(m_old - m_new)) over its keys, with the next two tiles' K/V loads in
-// flight while the current tile is computed; the 16 wave states are merged once in
-// LDS at the end:  out = sum_w e^(m_w - M) acc_w / sum_w e^(m_w - M) l_w.
+// Scores are kept in log2 units (q is pre-multiplied by log2(e) / sqrt(D)), so every
+// softmax weight is one exp2 of a score difference.  Every wave keeps its own online
+// softmax (running max m, sum l, accumulator rescaled by 2^(m_old - m_new) when the
+// maximum grows) over its keys, with the next two tiles' K/V loads in flight while
+// the current tile is computed; the 16 wave states are merged once in LDS at the
+// end:  out = sum_w 2^(m_w - M) acc_w / sum_w 2^(m_w - M) l_w.
 // The new token's key is rotated and rounded to bf16 like every cached entry; the
 // workgroup of the kv head's first query head writes it and the value to the cache,
 // the others use their own identical copy for that row.
@@ -111,8 +113,7 @@ __device__ __forceinline__ void attn_issue(AttnTile<D>& b, const uint16_t* __res
 template <int D>
 __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int len, int pos, int wave, int krow,
                                              int col, const float (&qv)[8], const uint16_t* s_knew,
-                                             const uint16_t* s_vnew, float scale, float& m_run, float& l_run,
-                                             float (&acc)[8]) {
+                                             const uint16_t* s_vnew, float& m_run, float& l_run, float (&acc)[8]) {
   using T = AttnTile<D>;
   float s[T::P];
   float m_tile = -INFINITY;
@@ -126,20 +127,24 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
     for (int u = 0; u < 4; ++u)
       d = fmaf(qv[2 * u + 1], bf16_bits_to_f32(w[u] >> 16), fmaf(qv[2 * u], bf16_bits_to_f32(w[u] & 0xffffu), d));
     d = group_sum<T::LPK>(d);
-    s[i] = key < len ? d * scale : -INFINITY;
+    s[i] = key < len ? d : -INFINITY;
     m_tile = fmaxf(m_tile, s[i]);
   }
+  // the maximum over every key of the wave: the same value in all lanes, so the
+  // rescale below is a uniform branch, taken only when the running maximum grows
   m_tile = stride_max<T::LPK>(m_tile);
-  const float m_new = fmaxf(m_run, m_tile);
-  if (m_new == -INFINITY) return;  // no valid key for this wave yet
-  const float alpha = expf(m_run - m_new);  // 0 while m_run is -inf
-  l_run *= alpha;
+  if (m_tile > m_run) {
+    const float alpha = exp2f(m_run - m_tile);  // 0 while m_run is -inf
+    l_run *= alpha;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+    m_run = m_tile;
+  }
+  if (m_run == -INFINITY) return;  // no valid key for this wave yet
 #pragma unroll
   for (int i = 0; i < T::P; ++i) {
     const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
-    const float p = s[i] == -INFINITY ? 0.0f : expf(s[i] - m_new);
+    const float p = exp2f(s[i] - m_run);  // masked keys: exp2(-inf) = 0
     l_run += p;
     // rows past the length may hold anything (even NaN): they must not reach acc
     const uint4 vr = key == pos ? *(const uint4*)(s_vnew + col * 8) : (key < len ? b.v[i] : make_uint4(0, 0, 0, 0));
@@ -150,19 +155,18 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
       acc[2 * u + 1] = fmaf(p, bf16_bits_to_f32(w[u] >> 16), acc[2 * u + 1]);
     }
   }
-  m_run = m_new;
 }
 
 // SPLIT > 1 (OUT 3): workgroup (head, sp) takes the tiles t = sp, sp + SPLIT, ... and
-// writes its partial state (m, l, 0, 0, acc[D]) -- acc not yet divided by l -- to
-// out_part[sp][head]; the consumer merges the SPLIT partials (act_producer.h,
-// SRC_ATTN2 / SRC_ATTN4).  A split with no tile writes m = -inf, l = 0, acc = 0.
+// writes its partial state (m, l, 0, 0, acc[D]) -- m in log2 units, acc not yet
+// divided by l -- to out_part[sp][head]; the consumer merges the SPLIT partials
+// (act_producer.h, SRC_ATTN2 / SRC_ATTN4).  A split with no tile writes m = -inf, l = 0, acc = 0.
 template <int D, int OUT, int SPLIT = 1>
 __global__ __launch_bounds__(1024) void attn_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
-    int max_seq, float scale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
+    int max_seq, float qscale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
     float* __restrict__ out_s, float* __restrict__ out_part, int xcd_map) {
   static_assert((OUT == 3) == (SPLIT > 1), "split partials go to out_part");
   using T = AttnTile<D>;
@@ -219,8 +223,8 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
 
   if (tid < HALF) {
     const float c = rope_cos[(size_t)pos * HALF + tid], sn = rope_sin[(size_t)pos * HALF + tid];
-    s_q[tid] = q0 * c - q1 * sn;
-    s_q[tid + HALF] = q0 * sn + q1 * c;
+    s_q[tid] = (q0 * c - q1 * sn) * qscale;
+    s_q[tid + HALF] = (q0 * sn + q1 * c) * qscale;
     s_knew[tid] = f32_to_bf16_bits(k0 * c - k1 * sn);
     s_knew[tid + HALF] = f32_to_bf16_bits(k0 * sn + k1 * c);
     s_vnew[tid] = f32_to_bf16_bits(v0);
@@ -242,15 +246,13 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   // a buffer is refilled only when a later tile of this workgroup remains: loads past
   // the last tile would only be waited for (their registers are reused by the merge)
   for (int j = 0; j < nt; j += 3) {
-    attn_compute<D>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run, acc);
+    attn_compute<D>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
     if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
     if (j + 1 < nt)
-      attn_compute<D>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run,
-                      acc);
+      attn_compute<D>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
     if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
     if (j + 2 < nt)
-      attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, scale, m_run, l_run,
-                      acc);
+      attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
     if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
   }
   // merge the rows of the wave (same columns), then the waves through LDS
@@ -266,18 +268,18 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     }
   }
   lds_barrier();
-  // wave weights e^(m_w - M) once (lanes 0..15 of wave 0), then every output column
+  // wave weights 2^(m_w - M) once (lanes 0..15 of wave 0), then every output column
   // is a plain weighted sum of the 16 wave accumulators
   if (tid < T::NW) {
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < T::NW; ++w) M = fmaxf(M, s_m[w]);
-    const float f = s_m[tid] == -INFINITY ? 0.0f : expf(s_m[tid] - M);
+    const float f = s_m[tid] == -INFINITY ? 0.0f : exp2f(s_m[tid] - M);
     s_f[tid] = f;
     if (tid == 0) {
       float L = 0.0f;
 #pragma unroll
-      for (int w = 0; w < T::NW; ++w) L = fmaf(s_m[w] == -INFINITY ? 0.0f : expf(s_m[w] - M), s_l[w], L);
+      for (int w = 0; w < T::NW; ++w) L = fmaf(s_m[w] == -INFINITY ? 0.0f : exp2f(s_m[w] - M), s_l[w], L);
       s_ml[0] = M;
       s_ml[1] = L;
     }
@@ -552,13 +554,15 @@ static hipError_t launch_rmsnorm(const nve_decode_config& c, const float* h, con
 
 static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_io& io, const DecodeWs& ws,
                                    bool w4a8, int split, hipStream_t s) {
-  const float scale = 1.0f / sqrtf((float)c.head_dim);
+  // scores in log2 units: q is pre-multiplied by log2(e) / sqrt(D), so the softmax
+  // weights are exp2 of score differences
+  const float qscale = 1.4426950408889634f / sqrtf((float)c.head_dim);
   // (kv head, split) pairs a multiple of 8: each XCD gets whole groups of query heads
   const int xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1;
 #define NVE_ATTN(D, OUT, S)                                                                                     \
   hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
                      ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,             \
-                     c.num_kv_heads, c.max_seq, scale, ws.act_bf16, ws.xq, ws.xs, ws.part, xcd_map)
+                     c.num_kv_heads, c.max_seq, qscale, ws.act_bf16, ws.xq, ws.xs, ws.part, xcd_map)
 #define NVE_ATTN_D(D)                    \
   if (split == 4) NVE_ATTN(D, 3, 4);     \
   else if (split == 2) NVE_ATTN(D, 3, 2); \
