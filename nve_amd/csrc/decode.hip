@@ -582,12 +582,14 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
 
 // Key splits of the fused decode attention (the partials are merged in the o_proj
 // GEMV's staging), chosen from the cache capacity: one workgroup streams about
-// 60 GB/s, so long caches need more workgroups per head, while at a few hundred keys
-// the merge costs more than the split saves.  NVE_ATTN_SPLIT=1/2/4 overrides.
+// 60 GB/s and computes one 128-key tile per head in about 1.3 us, so caches past a
+// few hundred keys need more workgroups per head; the merging o_proj launch uses few
+// workgroups, so four splits cost little more than two.  NVE_ATTN_SPLIT=1/2/4
+// overrides.
 static int attn_split(const nve_decode_config& c) {
   const char* e = getenv("NVE_ATTN_SPLIT");
   if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && e[1] == 0) return e[0] - '0';
-  return c.max_seq <= 512 ? 1 : (c.max_seq <= 2048 ? 2 : 4);
+  return c.max_seq <= 256 ? 1 : 4;
 }
 
 // Fused producers in the decode layer (RMSNorm into Q/K/V and gate/up, SiLU * up into

@@ -230,7 +230,7 @@ static hipError_t launch_w4a16_m(const void* x, W4Segs segs, int K, hipStream_t 
 
 template <int OUT_DT, int SRC, bool SWI>
 static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream) {
-  const W4Tiling t = choose_w4_tiling(segs, K);
+  const W4Tiling t = nve::attn_splits_of(SRC) ? choose_merge_tiling(segs, K) : choose_w4_tiling(segs, K);
   if (t.multi) return hipErrorInvalidValue;
   if (SWI) {
     const int R = t.R < 2 ? 2 : t.R;

@@ -220,7 +220,7 @@ static hipError_t launch_w4a8_dt(const int8_t* xq, const float* xs, W4Segs segs,
 // Fused-producer launches (one-shot kernels, one staging pass: K <= 16384).
 template <int OUT_DT, int SRC, bool SWI>
 static hipError_t launch_w4a8_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream) {
-  const W4Tiling t = choose_w4_tiling(segs, K);
+  const W4Tiling t = nve::attn_splits_of(SRC) ? choose_merge_tiling(segs, K) : choose_w4_tiling(segs, K);
   if (t.multi) return hipErrorInvalidValue;
   if (SWI) {
     const int R = t.R < 2 ? 2 : t.R;

@@ -43,6 +43,16 @@ inline W4Tiling choose_w4_tiling(const W4Segs& s, int K) {
   return W4Tiling{r, nj, multi};
 }
 
+// Launches whose staging merges the key-split attention partials (o_proj after split
+// attention): every workgroup reads the partial records of every head, so that work
+// grows with the number of workgroups; these take the largest R of the table for their
+// NJ (fewest workgroups) instead of filling 512 workgroups.
+inline W4Tiling choose_merge_tiling(const W4Segs& s, int K) {
+  W4Tiling t = choose_w4_tiling(s, K);
+  t.R = t.NJ == 1 ? 8 : (t.NJ == 2 ? 4 : (t.NJ <= 4 ? 2 : 1));
+  return t;
+}
+
 inline void finalize_segments(W4Segs& s, int R) {
   int wg = 0;
   for (int i = 0; i < 3; ++i) {
