@@ -438,7 +438,10 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool) -> d
            "bytes_per_token": wb + kvb,
            "GBs": round((wb + kvb) / (ms * 1e-3) / 1e9, 1),
            "frac_hbm_peak": round((wb + kvb) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-           "launches_per_token": None}
+           # per layer: Q/K/V (norm fused), attention, o_proj, gate/up (norm + SwiGLU fused),
+           # down; head: final norm, lm_head, argmax partials, argmax + next embedding
+           "launches_per_token": 5 * s.layers + 4,
+           "attn_key_split": int(os.environ.get("NVE_ATTN_SPLIT", 1 if m.max_seq <= 256 else 4))}
     log(f"decode 3B: {ms * 1e3:.1f} us/token, {tok_s:.1f} tok/s, {rec['GBs']} GB/s")
     if not no_cpu:
         import numpy as np
