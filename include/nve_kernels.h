@@ -242,8 +242,9 @@ int nve_hip_set_gemv_policy(int policy, int persistent_wg_per_cu, int persistent
  * scales, nve_quantize_f16_q8 semantics) or W4A16 (bf16 GEMV inputs).  Five launches
  * per layer: Q/K/V with the RMSNorm computed in its staging; attention (RoPE, cache
  * append, softmax, output converted to the o_proj input -- or, for caches of more than
- * 256 slots, split over 4 workgroups per head whose partial softmax states the o_proj
- * staging merges; NVE_ATTN_SPLIT=1/2/4 in the environment overrides); o_proj
+ * 256 slots, split over 4 workgroups per head (8 above 1024 slots when
+ * num_heads * head_dim <= 4096) whose partial softmax states the o_proj staging merges;
+ * NVE_ATTN_SPLIT=1/2/4/8 in the environment overrides); o_proj
  * with the residual add; gate/up with the RMSNorm in its staging and silu(gate) * up in its epilogue;
  * down with the residual add.  (NVE_DECODE_FUSE=0 in the environment selects
  * standalone RMSNorm / SiLU-mul kernels instead.)  The position of the token is read from

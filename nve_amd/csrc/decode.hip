@@ -160,7 +160,7 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
 // SPLIT > 1 (OUT 3): workgroup (head, sp) takes the tiles t = sp, sp + SPLIT, ... and
 // writes its partial state (m, l, 0, 0, acc[D]) -- m in log2 units, acc not yet
 // divided by l -- to out_part[sp][head]; the consumer merges the SPLIT partials
-// (act_producer.h, SRC_ATTN2 / SRC_ATTN4).  A split with no tile writes m = -inf, l = 0, acc = 0.
+// (act_producer.h, SRC_ATTN2 / 4 / 8).  A split with no tile writes m = -inf, l = 0, acc = 0.
 template <int D, int OUT, int SPLIT = 1>
 __global__ __launch_bounds__(1024) void attn_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -465,7 +465,9 @@ struct DecodeWs {
   size_t bytes;
 };
 
-constexpr int kMaxAttnSplit = 4;
+constexpr int kMaxAttnSplit = 8;
+// cache capacity above which the attention takes eight key splits (where they fit)
+constexpr int kAttnSplit8Slots = 1024;
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -564,7 +566,8 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
                      ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,             \
                      c.num_kv_heads, c.max_seq, qscale, ws.act_bf16, ws.xq, ws.xs, ws.part, xcd_map)
 #define NVE_ATTN_D(D)                    \
-  if (split == 4) NVE_ATTN(D, 3, 4);     \
+  if (split == 8) NVE_ATTN(D, 3, 8);     \
+  else if (split == 4) NVE_ATTN(D, 3, 4); \
   else if (split == 2) NVE_ATTN(D, 3, 2); \
   else if (w4a8) NVE_ATTN(D, 2, 1);      \
   else NVE_ATTN(D, 1, 1);
@@ -584,12 +587,16 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
 // GEMV's staging), chosen from the cache capacity: one workgroup streams about
 // 60 GB/s and computes one 128-key tile per head in about 1.3 us, so caches past a
 // few hundred keys need more workgroups per head; the merging o_proj launch uses few
-// workgroups, so four splits cost little more than two.  NVE_ATTN_SPLIT=1/2/4
-// overrides.
+// workgroups, so the merge costs little.  Eight splits hold 8 partial chunks in the
+// o_proj staging registers, which fits one staging pass (num_heads * head_dim <= 4096);
+// wider layers use four.  NVE_ATTN_SPLIT=1/2/4/8 overrides (8 only where it fits).
+static int attn_split_max(const nve_decode_config& c) { return c.num_heads * c.head_dim <= 4096 ? 8 : 4; }
+
 static int attn_split(const nve_decode_config& c) {
   const char* e = getenv("NVE_ATTN_SPLIT");
-  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && e[1] == 0) return e[0] - '0';
-  return c.max_seq <= 256 ? 1 : 4;
+  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4' || e[0] == '8') && e[1] == 0)
+    return e[0] - '0' < attn_split_max(c) ? e[0] - '0' : attn_split_max(c);
+  return c.max_seq <= 256 ? 1 : (c.max_seq <= kAttnSplit8Slots ? 4 : attn_split_max(c));
 }
 
 // Fused producers in the decode layer (RMSNorm into Q/K/V and gate/up, SiLU * up into
@@ -634,7 +641,7 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
   const int split = fuse ? attn_split(c) : 1;
   NVE_TRY(launch_attention(c, io, ws, w4a8, split, s));
   if (split > 1)
-    NVE_TRY(gemv_fused(w4a8, split == 4 ? nve::SRC_ATTN4 : nve::SRC_ATTN2, false,
+    NVE_TRY(gemv_fused(w4a8, split == 8 ? nve::SRC_ATTN8 : (split == 4 ? nve::SRC_ATTN4 : nve::SRC_ATTN2), false,
                        nve::ProdArgs{ws.part, nullptr, 0.0f, c.head_dim, c.num_heads}, one_seg(w.o, io.hidden),
                        NVE_DT_F32_ACCUM, QD, s));
   else

@@ -293,6 +293,8 @@ hipError_t launch_w4a16_fused(int src, bool swiglu, const nve::ProdArgs& pa, con
     return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, false>(pa, segs, K, stream);
   if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
     return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, false>(pa, segs, K, stream);
+  if (src == nve::SRC_ATTN8 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
+    return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN8, false>(pa, segs, K, stream);
   return hipErrorInvalidValue;
 }
 

@@ -270,6 +270,8 @@ hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, cons
     return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, false>(pa, segs, K, stream);
   if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM)
     return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, false>(pa, segs, K, stream);
+  if (src == nve::SRC_ATTN8 && out_dt == NVE_DT_F32_ACCUM)
+    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN8, false>(pa, segs, K, stream);
   // W4A8 GEMV quantizing its own 16-bit / f32 activations (fp16 or fp32 output)
 #define NVE_QX(SRC)                                                                    \
   if (src == SRC) {                                                                    \

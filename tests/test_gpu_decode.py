@@ -91,13 +91,13 @@ def _run_teacher_forced(torch, m, steps, token0=5):
     return m
 
 
-@pytest.mark.parametrize("fuse,split", [("1", "4"), ("1", "2"), ("1", "1"), ("0", "1")])
+@pytest.mark.parametrize("fuse,split", [("1", "8"), ("1", "4"), ("1", "2"), ("1", "1"), ("0", "1")])
 @pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256)])
 def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, split, monkeypatch):
     """Both layer paths: producers fused into the GEMV staging, and standalone
-    RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0); fused attention split over 1, 2 or
-    4 workgroups per head (at 61..66 keys most splits have no tile: their partials are
-    empty and must drop out of the merge)."""
+    RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0); fused attention split over 1, 2, 4
+    or 8 workgroups per head (at 61..66 keys most splits have no tile: their partials
+    are empty and must drop out of the merge)."""
     monkeypatch.setenv("NVE_DECODE_FUSE", fuse)
     monkeypatch.setenv("NVE_ATTN_SPLIT", split)
     m = _model(torch_dev, heads, kv, d)
@@ -138,7 +138,7 @@ def test_decode_graph_replay_matches_eager(torch_dev):
     assert int(m.pos.item()) == 40 + n
 
 
-@pytest.mark.parametrize("split", ["2", "4"])
+@pytest.mark.parametrize("split", ["2", "4", "8"])
 def test_decode_graph_replay_split_attention(torch_dev, split, monkeypatch):
     """Key-split attention (partials merged in the o_proj staging) under HIP graph
     replay: every replayed token and its logits equal the eager sequence bit for bit,
@@ -173,10 +173,11 @@ def test_decode_3b_shape_smoke(torch_dev, fuse, monkeypatch):
     _run_teacher_forced(torch_dev, m, steps=1)
 
 
-@pytest.mark.parametrize("split", ["1", "4"])
+@pytest.mark.parametrize("split", ["1", "4", "8"])
 def test_decode_long_cache(torch_dev, split, monkeypatch):
     """A cache of 8190+ keys: many tiles per workgroup (256 keys per tile at head_dim
-    64 -> 32 tiles, 8 per split at 4 splits), pos 8190..8192 crosses a tile edge."""
+    64 -> 32 tiles, 8 per split at 4 splits, 4 at 8), pos 8190..8192 crosses a tile
+    edge."""
     monkeypatch.setenv("NVE_ATTN_SPLIT", split)
     m = _model(torch_dev, 4, 2, 64, layers=2, importance=(0.0, 1.0), max_seq=8256, prefill=8190)
     _run_teacher_forced(torch_dev, m, steps=3)
