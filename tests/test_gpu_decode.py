@@ -92,7 +92,7 @@ def _run_teacher_forced(torch, m, steps, token0=5):
 
 
 @pytest.mark.parametrize("fuse,split", [("1", "8"), ("1", "4"), ("1", "2"), ("1", "1"), ("0", "1")])
-@pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256)])
+@pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256), (24, 8, 128)])
 def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, split, monkeypatch):
     """Both layer paths: producers fused into the GEMV staging, and standalone
     RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0); fused attention split over 1, 2, 4
