@@ -27,6 +27,11 @@ launches with HIP events on the stream it runs on.  cpu_baseline times the
 reference's CPU quantized GEMV (QuantizedTensor::matvec_f32 + q4_dot_row_avx2,
 restated in oracle/) on the host cores over a bounded sample.
 
+Also in the line (measured beside the step, not part of `value`): every suite shape
+timed on its own (graphs of 40 back-to-back launches over 8 weight copies; GB/s and
+GEMV/s), the same table at the Llama-3.2-1B shapes, the batched
+W4A8 sweep, the 3B decode step and the prefill GEMM.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
 from __future__ import annotations
@@ -56,6 +61,16 @@ SUITE_8B = [  # name, N, K
     ("lm_head", 128256, 4096),
 ]
 
+SUITE_1B = [  # BASELINE config 2 (Llama-3.2-1B layer shapes); reported beside the 8B suite
+    ("q_proj", 2048, 2048),
+    ("k_proj", 512, 2048),
+    ("v_proj", 512, 2048),
+    ("o_proj", 2048, 2048),
+    ("gate_proj", 8192, 2048),
+    ("up_proj", 8192, 2048),
+    ("down_proj", 2048, 8192),
+]
+
 
 def weight_bytes(n: int, k: int) -> int:
     return n * k // 2 + n * (k // 32) * 4
@@ -71,12 +86,12 @@ def log(*a):
 
 
 # ---------------------------------------------------------------------------
-def make_inputs(torch, hk, copies_layer: int, copies_head: int, seed: int = 0x4E5645):
+def make_inputs(torch, hk, copies_layer: int, copies_head: int, seed: int = 0x4E5645, suite=SUITE_8B):
     """Quantized weight copies for every suite shape (device-side generation)."""
     dev = "cuda"
     g = torch.Generator(device=dev).manual_seed(seed)
     weights = {}
-    for name, n, k in SUITE_8B:
+    for name, n, k in suite:
         c = copies_head if name == "lm_head" else copies_layer
         sets = []
         for _ in range(c):
@@ -227,12 +242,15 @@ def time_graphs(torch, graphs, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
+def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40, suite=SUITE_8B):
     """Average launch duration of every (shape, precision) GEMV, each timed on its own in
-    a graph of back-to-back launches over rotating weight copies."""
+    a graph of back-to-back launches over rotating weight copies.  acts: fp16 / bf16
+    activations keyed "h16" / "hb" (the hidden size) and "mid16" / "midb" (the FFN
+    size, down_proj's K)."""
     rows = {}
     s_bufs = {}
-    for name, n, k in SUITE_8B:
+    hid = [k for nm, _, k in suite if nm == "q_proj"][0]
+    for name, n, k in suite:
         sets = weights[name]
         for prec in ("w4a8", "w4a16"):
             odt_t = torch.float32 if name == "lm_head" else (torch.float16 if prec == "w4a8" else torch.bfloat16)
@@ -241,7 +259,7 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
             if prec == "w4a8":
                 xq = torch.empty(k, dtype=torch.int8, device="cuda")
                 xs = torch.empty(k // 32, dtype=torch.float32, device="cuda")
-                x16 = acts["mid16"] if k == 14336 else acts["h16"]
+                x16 = acts["h16"] if k == hid else acts["mid16"]
                 assert L.nve_hip_quantize_q8(x16.data_ptr(), 0, 1, k, xq.data_ptr(), xs.data_ptr(), None) == 0
 
                 def body(sets=sets, xq=xq, xs=xs, out=out, odt=odt, n=n, k=k):
@@ -251,7 +269,7 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
                         assert L.nve_hip_matvec_w4a8(xq.data_ptr(), xs.data_ptr(), nib.data_ptr(), sc.data_ptr(),
                                                      out.data_ptr(), odt, n, k, s) == 0
             else:
-                xb = acts["midb"] if k == 14336 else acts["hb"]
+                xb = acts["hb"] if k == hid else acts["midb"]
 
                 def body(sets=sets, xb=xb, out=out, odt=odt, n=n, k=k):
                     s = torch.cuda.current_stream().cuda_stream
@@ -268,7 +286,7 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
             ob = 4 if name == "lm_head" else 2
             b = gemv_bytes(n, k, prec, ob)
             rows[f"{name}/{prec}"] = {
-                "N": n, "K": k, "us": round(us, 3), "bytes": b,
+                "N": n, "K": k, "us": round(us, 3), "gemv_per_s": round(1e6 / us), "bytes": b,
                 "GBs": round(b / us / 1e3, 1), "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
             }
             s_bufs[(name, prec)] = (g, out)
@@ -276,9 +294,9 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
     # grouped launches (one launch for matrices sharing the input)
     from nve_amd._lib import W4Mat
     for label, names in (("qkv_grouped", ("q_proj", "k_proj", "v_proj")), ("gate_up_grouped", ("gate_proj", "up_proj"))):
-        k = 4096
+        k = hid
         for prec in ("w4a8", "w4a16"):
-            outs = [torch.empty([n for nm, n, _ in SUITE_8B if nm == x][0], dtype=torch.float16 if prec == "w4a8"
+            outs = [torch.empty([n for nm, n, _ in suite if nm == x][0], dtype=torch.float16 if prec == "w4a8"
                                 else torch.bfloat16, device="cuda") for x in names]
             xq = torch.empty(k, dtype=torch.int8, device="cuda")
             xs = torch.empty(k // 32, dtype=torch.float32, device="cuda")
@@ -304,9 +322,10 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40):
             g = capture(torch, body)
             time_graphs(torch, [g], 2)
             us = time_graphs(torch, [g], 10) * 1e3 / launches_per_graph
-            b = sum(gemv_bytes([n for nm, n, _ in SUITE_8B if nm == x][0], k, prec, 2) for x in names)
+            b = sum(gemv_bytes([n for nm, n, _ in suite if nm == x][0], k, prec, 2) for x in names)
             b -= (len(names) - 1) * ((k + (k // 32) * 4) if prec == "w4a8" else 2 * k)  # one shared input
-            rows[f"{label}/{prec}"] = {"N": sum(o.numel() for o in outs), "K": k, "us": round(us, 3), "bytes": b,
+            rows[f"{label}/{prec}"] = {"N": sum(o.numel() for o in outs), "K": k, "us": round(us, 3),
+                                       "gemv_per_s": round(1e6 / us), "bytes": b,
                                        "GBs": round(b / us / 1e3, 1), "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
             log(f"  {label:15s} {prec:6s} {us:8.2f} us {b / us / 1e3:8.1f} GB/s {100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}%")
     return rows
@@ -630,6 +649,17 @@ def main():
     rot_gb = round(sum(weight_bytes(n, k) * len(weights[nm]) for nm, n, k in SUITE_8B) / 1e9, 2)
     del weights, step, graphs
     torch.cuda.empty_cache()
+    # the Llama-3.2-1B layer shapes, same method (16 weight copies)
+    log("per-kernel table, Llama-3.2-1B shapes:")
+    w1b = make_inputs(torch, hk, 16, 1, seed=0x4E5646, suite=SUITE_1B)
+    acts1b = {}
+    for nm, k, sd in (("h", 2048, 11), ("mid", 8192, 14)):
+        x = make_activation(torch, k, sd)
+        acts1b[nm + "16"] = x.to(torch.float16)
+        acts1b[nm + "b"] = x.to(torch.bfloat16)
+    table_1b = kernel_table(torch, L, w1b, acts1b, suite=SUITE_1B)
+    del w1b, acts1b
+    torch.cuda.empty_cache()
     decode = None if args.no_decode else decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens,
                                                    args.no_cpu)
     log("prefill W4A16 GEMM:")
@@ -684,6 +714,7 @@ def main():
         "suite_8b_aggregate_GBs": {"w4a8_layers": agg("w4a8", layer_names), "w4a16_layers": agg("w4a16", layer_names),
                                    "w4a8_all": agg("w4a8", [n for n, _, _ in SUITE_8B]),
                                    "w4a16_all": agg("w4a16", [n for n, _, _ in SUITE_8B])},
+        "suite_1b": table_1b,
         "hbm_stream_probe_GBs": round(stream_gbs, 1),
         "batched_w4a8_8b": sweep,
         "decode_3b": decode,
