@@ -541,6 +541,38 @@ def decode_traffic_probe(torch) -> None:
     log(f"decode traffic probe: 6 steps, algorithmic bytes per step {m.step_bytes()}")
 
 
+def batched_probe(torch, L, hk):
+    """Short eager run for rocprofv3 --pmc of the batched W4A8 kernels (MFMA counters):
+    the configs[3] shapes (8B gate and down) at M in {1, 2, 4, 8, 16}, 10 launches each
+    over 4 weight copies, in the order printed."""
+    import numpy as np
+    g = torch.Generator(device="cuda").manual_seed(12)
+    order = []
+    for name in ("gate_proj", "down_proj"):
+        n, k = [(nn, kk) for nm, nn, kk in SUITE_8B if nm == name][0]
+        sets = []
+        for _ in range(4):
+            w = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+            sets.append(hk.q4_quantize(w))
+            del w
+        for m in (1, 2, 4, 8, 16):
+            r = np.random.default_rng(100 + m)
+            x = torch.from_numpy(r.standard_normal((m, k)).astype(np.float32)).cuda().to(torch.bfloat16)
+            xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+            xs = torch.empty(m, dtype=torch.bfloat16, device="cuda")
+            assert L.nve_hip_quantize_q8_rows(x.data_ptr(), 1, m, k, xq.data_ptr(), xs.data_ptr(), None) == 0
+            out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(10):
+                nib, sc = sets[i % 4]
+                assert L.nve_hip_matvec_w4a8_batched(m, xq.data_ptr(), xs.data_ptr(), 1, nib.data_ptr(), sc.data_ptr(),
+                                                     out.data_ptr(), 0, n, k, s) == 0
+            torch.cuda.synchronize()
+            order.append({"shape": name, "N": n, "K": k, "M": m, "launches": 10})
+        del sets
+    print(json.dumps({"probe": "batched", "order": order}), flush=True)
+
+
 def traffic_probe(torch, L, hk):
     """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
     256 MiB (calibration: 256 MiB read + 256 MiB written), then 5 launches of the
@@ -587,6 +619,8 @@ def main():
                     help="run only the 3B decode measurement (for profiling; no bench line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no bench line)")
+    ap.add_argument("--batched-probe", action="store_true",
+                    help="eager batched W4A8 launches for rocprofv3 --pmc MFMA counters (no bench line)")
     ap.add_argument("--decode-traffic-probe", action="store_true",
                     help="6 eager (not graph-replayed) 3B decode steps for rocprofv3 --pmc (no bench line)")
     args = ap.parse_args()
@@ -606,6 +640,9 @@ def main():
         return
     if args.decode_traffic_probe:
         decode_traffic_probe(torch)
+        return
+    if args.batched_probe:
+        batched_probe(torch, L, hk)
         return
     if args.decode_only:
         print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True)}))
