@@ -424,16 +424,29 @@ def cpu_baseline(target_s: float = 12.0) -> dict:
                       f"{threads} threads; GB/s over the same algorithmic bytes as the GPU"}
 
 
-def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool) -> dict:
+def attn_key_split(shape, max_seq: int) -> int:
+    """The key split the library's decode attention takes (decode.hip attn_split): 1 up
+    to 256 cache slots, 4 up to 1024, else 8 when num_heads * head_dim <= 4096 (else 4);
+    NVE_ATTN_SPLIT overrides, capped the same way."""
+    cap = 8 if shape.heads * shape.head_dim <= 4096 else 4
+    e = os.environ.get("NVE_ATTN_SPLIT")
+    if e in ("1", "2", "4", "8"):
+        return min(int(e), cap)
+    return 1 if max_seq <= 256 else (4 if max_seq <= 1024 else cap)
+
+
+def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, prefill: int = 512,
+              max_seq: int = 1024) -> dict:
     """synthetic Llama-3.2-3B decode at batch 1, greedy.  28 layers
     (a seeded 30% = 8 W4A16, 20 W4A8; W4A8 lm_head), 512 prefilled N(0,1) bf16 KV
     positions, one HIP graph per token (all layers + head, position device-resident),
     `tokens` greedy tokens timed with HIP events on the replay stream.  The CPU leg runs
     the reference's CPU decode path (Q4 x f32 matvec_f32, AVX2 restated in oracle/, all
-    projections; f32 attention) on the same weights for `cpu_tokens` tokens."""
+    projections; f32 attention) on the same weights for `cpu_tokens` tokens.  prefill /
+    max_seq: the cached positions and the cache capacity (also run at 7000 / 8192 as
+    the long-context line, GPU only)."""
     from nve_amd.decode import LLAMA_3_2_3B, DecodeModel
     s = LLAMA_3_2_3B
-    prefill, max_seq = 512, 1024
     tokens = min(tokens, max_seq - prefill - warm - 1)
     m = DecodeModel(s, max_seq=max_seq, prefill=prefill)
     m.capture()
@@ -453,14 +466,14 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool) -> d
     tok_s = 1e3 / ms
     n16 = sum(1 for u in m.use_w4a8 if not u)
     rec = {"tok_per_s": round(tok_s, 1), "ms_per_token": round(ms, 4), "tokens": tokens, "warmup": warm,
-           "layers_w4a8": s.layers - n16, "layers_w4a16": n16, "kv_prefill": prefill,
+           "layers_w4a8": s.layers - n16, "layers_w4a16": n16, "kv_prefill": prefill, "kv_capacity": max_seq,
            "bytes_per_token": wb + kvb,
            "GBs": round((wb + kvb) / (ms * 1e-3) / 1e9, 1),
            "frac_hbm_peak": round((wb + kvb) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            # per layer: Q/K/V (norm fused), attention, o_proj, gate/up (norm + SwiGLU fused),
            # down; head: final norm, lm_head, argmax partials, argmax + next embedding
            "launches_per_token": 5 * s.layers + 4,
-           "attn_key_split": int(os.environ.get("NVE_ATTN_SPLIT", 1 if m.max_seq <= 256 else 4))}
+           "attn_key_split": attn_key_split(s, max_seq)}
     log(f"decode 3B: {ms * 1e3:.1f} us/token, {tok_s:.1f} tok/s, {rec['GBs']} GB/s")
     if not no_cpu:
         import numpy as np
@@ -699,6 +712,10 @@ def main():
     torch.cuda.empty_cache()
     decode = None if args.no_decode else decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens,
                                                    args.no_cpu)
+    decode_long = None
+    if not args.no_decode:
+        torch.cuda.empty_cache()
+        decode_long = decode_3b(torch, 128, 8, 0, True, prefill=7000, max_seq=8192)
     log("prefill W4A16 GEMM:")
     prefill = prefill_gemm(torch, hk)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -755,6 +772,7 @@ def main():
         "hbm_stream_probe_GBs": round(stream_gbs, 1),
         "batched_w4a8_8b": sweep,
         "decode_3b": decode,
+        "decode_3b_long_context": decode_long,
         "prefill_w4a16_gemm": prefill,
     }
     print(json.dumps(rec), flush=True)
