@@ -505,7 +505,9 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     against the reference's own method on the same GPU
     (nve_dequant_w4a16 to fp16, then a dense fp16 GEMM -- torch.matmul, i.e. the
     vendor BLAS -- as GpuWeight::matmul_x does with candle, src/gpu_layer.rs:219-237).
-    Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time."""
+    Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time.
+    library_us: nve_hip_gemm_w4a16_ws with its workspace (dequant + hipBLASLt from
+    M = 512 on, the fused kernels below)."""
     g = torch.Generator(device="cuda").manual_seed(17)
     n, k = 14336, 4096
     nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
@@ -532,12 +534,18 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
 
         us = timed(lambda: hk.gemm_w4a16(x, nib, sc, n, k))
         us_ref = timed(lambda: hk.dequant_w4(nib, sc, n, k)) + timed(lambda: torch.matmul(x, wf.t()))
+        wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda") if wsb else None
+        us_lib = timed(lambda: hk.gemm_w4a16_ws(x, nib, sc, n, k, ws))
         fl = 2.0 * m * n * k
         out["rows"].append({"M": m, "fused_us": round(us, 1), "fused_TFLOPs": round(fl / us / 1e6, 1),
                             "frac_mfma_peak": round(fl / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
-                            "dequant_plus_blas_us": round(us_ref, 1)})
-        log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us")
-        del x, wf
+                            "dequant_plus_blas_us": round(us_ref, 1),
+                            "library_us": round(us_lib, 1),
+                            "library_path": "dequant + hipBLASLt" if wsb else "fused"})
+        log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us, "
+            f"nve_hip_gemm_w4a16_ws {us_lib:.1f} us")
+        del x, wf, ws
     return out
 
 

@@ -5,8 +5,9 @@
  *
  * Conventions (all entry points):
  *   - Every pointer is a device pointer the caller allocated; nothing here allocates
- *     device memory, and every launch is asynchronous on `stream` (a hipStream_t;
- *     NULL = the default stream).
+ *     device memory (except the hipBLASLt handle nve_hip_gemm_w4a16_ws creates once per
+ *     device), and every launch is asynchronous on `stream` (a hipStream_t; NULL = the
+ *     default stream).
  *   - Weights use the reference's GPU layout (QuantizedTensor::extract_for_gpu,
  *     src/quantize.rs:437-463): nibbles u8 [N, K/2], byte j of each 32-weight block
  *     = element j (low nibble) | element j+16 (high nibble); scales f32 [N, K/32];
@@ -218,6 +219,19 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * BF16 or F32.  K % 64 == 0. */
 int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,
                        const float *awq, void *out, int out_dtype, int N, int K, void *stream);
+
+/* The same product with the reference's own two-step method where it is faster
+ * (GpuWeight::matmul_x, src/gpu_layer.rs:219-237): for M >= 512, with a workspace of at
+ * least nve_hip_gemm_w4a16_workspace_bytes(M, N, K) bytes (256-byte aligned) and out
+ * F32 or x's dtype, the weights are dequantized into the workspace (nve_hip_dequant_w4,
+ * bit-identical to the reference dequant) and multiplied by hipBLASLt (fp32
+ * accumulation); otherwise it runs nve_hip_gemm_w4a16.  The first call per device and
+ * shape creates the hipBLASLt handle and selects the algorithm, so make it outside
+ * graph capture.  No counterpart in the reference's FFI (it makes two calls). */
+size_t nve_hip_gemm_w4a16_workspace_bytes(int M, int N, int K);
+int nve_hip_gemm_w4a16_ws(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,
+                          const float *awq, void *out, int out_dtype, int N, int K, void *workspace,
+                          size_t workspace_bytes, void *stream);
 
 /* ---- per-layer precision dispatch (src/gpu_layer.rs:1013-1025) -------------- */
 /* Returns 1 (W4A8) when NVE_NO_W4A8 is unset and layer_importance < threshold,

@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_q4_repack": (_i, [_p, _i, _i, _p, _p, _p]),
     "nve_hip_dequant_w4": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
     "nve_hip_gemm_w4a16": (_i, [_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "nve_hip_gemm_w4a16_workspace_bytes": (C.c_size_t, [_i, _i, _i]),
+    "nve_hip_gemm_w4a16_ws": (_i, [_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _p, C.c_size_t, _p]),
     "nve_dequant_w4a16": (None, [_p, _p, _p, _p, _i, _i, _p]),
     "nve_use_w4a8": (_i, [C.c_double]),
     "nve_hip_stream_read": (_i, [_p, C.c_size_t, _p, _p]),

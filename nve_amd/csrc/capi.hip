@@ -56,6 +56,10 @@ hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib,
                              void* out, int out_dt, int N, int K, hipStream_t s);
 hipError_t launch_dequant_w4(const uint8_t* nib, const float* scales, const float* awq, void* out, int out_dt,
                              int N, int K, hipStream_t stream);
+size_t gemm_w4a16_ws_bytes(int M, int N, int K);
+hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
+                                const float* awq, void* out, int out_dt, int N, int K, void* ws, size_t ws_bytes,
+                                hipStream_t s);
 hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, float* scales,
                             hipStream_t stream);
 hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream);
@@ -317,6 +321,25 @@ int nve_hip_gemm_w4a16(const void* x, int x_dtype, int M, const uint8_t* nibbles
       !aligned(out, out_dtype == NVE_DT_F32 ? 4 : 2))
     return set_status(NVE_ERR_ALIGN);
   return from_hip(launch_gemm_w4a16(x, x_dtype, M, nibbles, scales, awq, out, out_dtype, N, K, (hipStream_t)stream));
+}
+
+size_t nve_hip_gemm_w4a16_workspace_bytes(int M, int N, int K) {
+  return (M < 1 || N < 1 || K < 64) ? 0 : gemm_w4a16_ws_bytes(M, N, K);
+}
+
+int nve_hip_gemm_w4a16_ws(const void* x, int x_dtype, int M, const uint8_t* nibbles, const float* scales,
+                          const float* awq, void* out, int out_dtype, int N, int K, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (!x || !nibbles || !scales || !out) return set_status(NVE_ERR_NULL);
+  if (x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) return set_status(NVE_ERR_DTYPE);
+  if (out_dtype != NVE_DT_F16 && out_dtype != NVE_DT_BF16 && out_dtype != NVE_DT_F32) return set_status(NVE_ERR_DTYPE);
+  if (M < 1 || N < 1 || K < 64 || K % 64 != 0) return set_status(NVE_ERR_SHAPE);
+  if (K > NVE_MAX_K) return set_status(NVE_ERR_TOO_LARGE);
+  if (!aligned(x, 16) || !aligned(nibbles, 16) || !aligned(scales, 4) || (awq && !aligned(awq, 16)) ||
+      !aligned(out, out_dtype == NVE_DT_F32 ? 4 : 2) || (workspace && !aligned(workspace, 256)))
+    return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_gemm_w4a16_ws(x, x_dtype, M, nibbles, scales, awq, out, out_dtype, N, K, workspace,
+                                       workspace_bytes, (hipStream_t)stream));
 }
 
 // ---- dispatch -------------------------------------------------------------------------

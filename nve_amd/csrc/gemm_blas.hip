@@ -1,0 +1,163 @@
+// gemm_blas.hip -- the reference's own prefill method for large M.
+//
+// GpuWeight::matmul_x (src/gpu_layer.rs:219-237) expands the int4 weights to a dense
+// 16-bit matrix with nve_dequant_w4a16 and multiplies with the vendor GEMM.  The fused
+// kernel of gemm_w4a16.hip wins while weight traffic dominates (M <= ~128) but
+// re-dequantizes each weight slice once per 128-row tile, so from M = 512 on the
+// reference's two-step method is the faster one on this part.  nve_hip_gemm_w4a16_ws
+// takes that path when the caller provides the workspace: the weights are dequantized
+// into it (dequant_w4_kernel, bit-identical to the reference dequant) and hipBLASLt
+// computes Y = X W^T with fp32 accumulation.  Column-major view: D (N x M, ld N) =
+// op(A) op(B) with A = the dequantized W seen as K x N (ld K, transposed) and B = X
+// seen as K x M (ld K), which is the row-major Y [M, N].
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "common.h"
+#include "w4_launch.h"
+
+namespace nve_host {
+
+hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, const float* awq,
+                             void* out, int out_dt, int N, int K, hipStream_t s);
+hipError_t launch_dequant_w4(const uint8_t* nib, const float* scales, const float* awq, void* out, int out_dt,
+                             int N, int K, hipStream_t stream);
+
+namespace {
+
+constexpr int kGemmBlasMinM = 512;        // from here on dequant + GEMM is faster
+constexpr size_t kBlasWorkspace = 32u << 20;
+constexpr int kBlasCandidates = 8;  // heuristic candidates timed on the first call per shape
+
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+hipDataType blas_type(int nve_dt) {
+  return nve_dt == NVE_DT_F16 ? HIP_R_16F : (nve_dt == NVE_DT_BF16 ? HIP_R_16BF : HIP_R_32F);
+}
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;                                     // per device
+std::map<std::tuple<int, int, int, int, int, int>, hipblasLtMatmulAlgo_t> g_algo;  // dev, M, N, K, x, out
+
+struct Descs {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  ~Descs() {
+    if (d) hipblasLtMatrixLayoutDestroy(d);
+    if (b) hipblasLtMatrixLayoutDestroy(b);
+    if (a) hipblasLtMatrixLayoutDestroy(a);
+    if (op) hipblasLtMatmulDescDestroy(op);
+  }
+};
+
+bool make_descs(Descs& ds, int M, int N, int K, int x_dt, int out_dt) {
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  return hipblasLtMatmulDescCreate(&ds.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatmulDescSetAttribute(ds.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) ==
+             HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatmulDescSetAttribute(ds.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) ==
+             HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatrixLayoutCreate(&ds.a, blas_type(x_dt), K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatrixLayoutCreate(&ds.b, blas_type(x_dt), K, M, K) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatrixLayoutCreate(&ds.d, blas_type(out_dt), N, M, N) == HIPBLAS_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+size_t gemm_w4a16_ws_bytes(int M, int N, int K) {
+  if (M < kGemmBlasMinM) return 0;
+  return round256((size_t)N * K * 2) + kBlasWorkspace;
+}
+
+// Dequant + hipBLASLt when M >= kGemmBlasMinM, the workspace is large enough and the
+// output is F32 or x's dtype; otherwise the fused kernel.  The first call per device and
+// shape creates the hipBLASLt handle and picks the fastest of up to kBlasCandidates
+// heuristic algorithms by timing them on the caller's stream (not under graph capture).
+hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
+                                const float* awq, void* out, int out_dt, int N, int K, void* ws, size_t ws_bytes,
+                                hipStream_t s) {
+  const size_t need = gemm_w4a16_ws_bytes(M, N, K);
+  if (need == 0 || ws == nullptr || ws_bytes < need || (out_dt != NVE_DT_F32 && out_dt != x_dt))
+    return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  hipblasLtHandle_t h = nullptr;
+  hipblasLtMatmulAlgo_t algo;
+  Descs ds;
+  if (!make_descs(ds, M, N, K, x_dt, out_dt)) return hipErrorNotSupported;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto hi = g_handles.find(dev);
+    if (hi == g_handles.end()) {
+      if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotSupported;
+      g_handles[dev] = h;
+    } else {
+      h = hi->second;
+    }
+    const auto key = std::make_tuple(dev, M, N, K, x_dt, out_dt);
+    auto ai = g_algo.find(key);
+    if (ai == g_algo.end()) {
+      hipblasLtMatmulPreference_t pref = nullptr;
+      const uint64_t wsz = kBlasWorkspace;
+      hipblasLtMatmulHeuristicResult_t res[kBlasCandidates];
+      int found = 0;
+      const bool ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+                      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz,
+                                                            sizeof wsz) == HIPBLAS_STATUS_SUCCESS &&
+                      hipblasLtMatmulAlgoGetHeuristic(h, ds.op, ds.a, ds.b, ds.d, ds.d, pref, kBlasCandidates, res,
+                                                      &found) == HIPBLAS_STATUS_SUCCESS &&
+                      found > 0;
+      if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+      // no algorithm for this shape: the fused kernel serves it
+      if (!ok) return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
+      int best = 0;
+      if (found > 1) {
+        // first call for this shape: time the candidates on the caller's stream (the
+        // product is recomputed below, so `out` only holds scratch until then)
+        e = launch_dequant_w4(nib, sc, awq, ws, x_dt, N, K, s);
+        if (e != hipSuccess) return e;
+        void* bws = (char*)ws + round256((size_t)N * K * 2);
+        const float alpha = 1.0f, beta = 0.0f;
+        hipEvent_t e0, e1;
+        if (hipEventCreate(&e0) != hipSuccess) return hipErrorNotSupported;
+        if (hipEventCreate(&e1) != hipSuccess) { hipEventDestroy(e0); return hipErrorNotSupported; }
+        float best_ms = 1e30f;
+        for (int c = 0; c < found; ++c) {
+          if (res[c].state != HIPBLAS_STATUS_SUCCESS || res[c].workspaceSize > kBlasWorkspace) continue;
+          bool run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d,
+                                        &res[c].algo, bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+          hipEventRecord(e0, s);
+          for (int r = 0; run_ok && r < 3; ++r)
+            run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d,
+                                     &res[c].algo, bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+          hipEventRecord(e1, s);
+          float ms = 1e30f;
+          if (hipEventSynchronize(e1) == hipSuccess && run_ok) hipEventElapsedTime(&ms, e0, e1);
+          if (run_ok && ms < best_ms) {
+            best_ms = ms;
+            best = c;
+          }
+        }
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+      }
+      ai = g_algo.emplace(key, res[best].algo).first;
+    }
+    algo = ai->second;
+  }
+  void* wdq = ws;
+  void* blas_ws = (char*)ws + round256((size_t)N * K * 2);
+  e = launch_dequant_w4(nib, sc, awq, wdq, x_dt, N, K, s);
+  if (e != hipSuccess) return e;
+  const float alpha = 1.0f, beta = 0.0f;
+  if (hipblasLtMatmul(h, ds.op, &alpha, wdq, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d, &algo, blas_ws,
+                      kBlasWorkspace, s) != HIPBLAS_STATUS_SUCCESS)
+    return hipErrorLaunchFailure;
+  return hipGetLastError();
+}
+
+}  // namespace nve_host

@@ -266,6 +266,27 @@ def gemm_w4a16(x: torch.Tensor, nibbles: torch.Tensor, scales: torch.Tensor, n: 
     return out
 
 
+def gemm_w4a16_workspace_bytes(m: int, n: int, k: int) -> int:
+    """Workspace that lets gemm_w4a16_ws take the dequant + hipBLASLt path (0: it will not)."""
+    return int(lib().nve_hip_gemm_w4a16_workspace_bytes(m, n, k))
+
+
+def gemm_w4a16_ws(x: torch.Tensor, nibbles: torch.Tensor, scales: torch.Tensor, n: int, k: int,
+                  workspace: torch.Tensor | None, awq: torch.Tensor | None = None,
+                  out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """gemm_w4a16 with the reference's two-step method (dequant + vendor GEMM) where it
+    is faster (M >= 512, given `workspace` of gemm_w4a16_workspace_bytes bytes)."""
+    m = x.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    ws_ptr = None if workspace is None else _dev(workspace, "workspace")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check("nve_hip_gemm_w4a16_ws",
+          lib().nve_hip_gemm_w4a16_ws(_dev(x, "x"), _dt(x), m, _dev(nibbles, "nibbles"), _dev(scales, "scales"),
+                                      None if awq is None else _dev(awq, "awq"), out.data_ptr(), _dt(out), n, k,
+                                      ws_ptr, ws_bytes, _stream()))
+    return out
+
+
 def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
     """HBM streaming probe (reads every byte of buf once)."""
     check("nve_hip_stream_read",

@@ -123,3 +123,52 @@ def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
                       out_dtype=out_dt)
     torch.cuda.synchronize()
     assert rel_err_floor(y.float().cpu().numpy(), ref) <= tol
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 256, 1024), (600, 520, 2048), (1024, 384, 4096)])
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("with_awq", [False, True])
+def test_gemm_w4a16_ws_blas_path(orc, torch_dev, hk, m, n, k, xdt, with_awq):
+    """nve_hip_gemm_w4a16_ws at M >= 512 with its workspace: dequant (bit-identical
+    weights) + hipBLASLt, the reference's own prefill method, to the same bar."""
+    torch = torch_dev
+    print(f"gemm_ws m={m} n={n} k={k} x={xdt} awq={with_awq}", flush=True)
+    rng = np.random.default_rng(m + 3 * n + k)
+    data = orc.q4_from_f32(weights(n, k, seed=m + 2 * n, std=0.05))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    awq = rng.uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
+    wref = _round(orc.q4_to_f32(data, n, k, awq), xdt).astype(np.float64)
+    x = _round(rng.standard_normal((m, k)).astype(np.float32), xdt)
+    ref = x.astype(np.float64) @ wref.T
+    tdt = torch.float16 if xdt == "f16" else torch.bfloat16
+    xt = torch.from_numpy(x).cuda().to(tdt)
+    wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
+    assert wsb >= n * k * 2
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    args = (xt, torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda(), n, k, ws,
+            None if awq is None else torch.from_numpy(awq).cuda())
+    y = hk.gemm_w4a16_ws(*args, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err_floor(y.cpu().numpy().astype(np.float64), ref) <= 2e-3
+    # the workspace holds the reference dequant of the weights, bit for bit
+    wdq = ws[: n * k * 2].view(tdt).view(n, k).float().cpu().numpy()
+    assert np.array_equal(wdq, wref.astype(np.float32))
+    # output in x's dtype: the fp32 result rounded once
+    y16 = hk.gemm_w4a16_ws(*args, out_dtype=tdt).float().cpu().numpy().astype(np.float64)
+    assert rel_err_floor(y16, ref) <= 2e-3 + (2.0 ** -8 if xdt == "bf16" else 2.0 ** -11)
+
+
+def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
+    """Below M = 512, or without a workspace, nve_hip_gemm_w4a16_ws is the fused kernel
+    (compared at fp16 output: fp32 output at small M splits K with atomic adds, whose
+    order is not fixed)."""
+    torch = torch_dev
+    assert hk.gemm_w4a16_workspace_bytes(511, 256, 1024) == 0 and hk.gemm_w4a16_workspace_bytes(512, 256, 1024) > 0
+    n, k = 256, 1024
+    data = orc.q4_from_f32(weights(n, k, seed=5, std=0.05))
+    nib, sc = (torch.from_numpy(a).cuda() for a in orc.extract_for_gpu(data, n, k))
+    for m in (64, 600):
+        x = torch.randn((m, k), device="cuda").to(torch.float16)
+        a = hk.gemm_w4a16(x, nib, sc, n, k, out_dtype=torch.float16).cpu()
+        b = hk.gemm_w4a16_ws(x, nib, sc, n, k, None, out_dtype=torch.float16).cpu()
+        assert torch.equal(a, b), m
