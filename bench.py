@@ -768,6 +768,9 @@ def main():
             "unit": "GB/s",
             "frac": round(head["GBs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            # the second denominator: the in-repo streaming-read probe on this GPU
+            "achievable_peak": round(stream_gbs, 1),
+            "frac_of_achievable": round(head["GBs"] / stream_gbs, 4),
             "bytes_per_launch": head["bytes"],
             "us_per_launch": head["us"],
         },
