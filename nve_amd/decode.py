@@ -83,13 +83,95 @@ def _w4(t: tuple[torch.Tensor, torch.Tensor], n: int, k: int) -> W4Weight:
     return W4Weight(t[0].data_ptr(), t[1].data_ptr(), n, k)
 
 
+def shape_from_hf_config(cfg: dict) -> ModelShape:
+    """ModelShape from a Hugging Face Llama config.json dict (the fields the reference's
+    src/config.rs reads: hidden_size, num_hidden_layers, num_attention_heads,
+    num_key_value_heads, head_dim, intermediate_size, vocab_size, rms_norm_eps,
+    rope_theta, rope_scaling with rope_type "llama3")."""
+    heads = int(cfg["num_attention_heads"])
+    hidden = int(cfg["hidden_size"])
+    rs = cfg.get("rope_scaling") or None
+    scaling = None
+    if rs and rs.get("rope_type", rs.get("type")) == "llama3":
+        scaling = RopeScaling(float(rs["factor"]), float(rs.get("low_freq_factor", 1.0)),
+                              float(rs.get("high_freq_factor", 4.0)),
+                              int(rs.get("original_max_position_embeddings", 8192)))
+    elif rs:
+        raise ValueError(f"rope_scaling {rs} is not supported (llama3 only)")
+    return ModelShape(hidden=hidden, layers=int(cfg["num_hidden_layers"]), heads=heads,
+                      kv_heads=int(cfg.get("num_key_value_heads", heads)),
+                      head_dim=int(cfg.get("head_dim") or hidden // heads), ffn=int(cfg["intermediate_size"]),
+                      vocab=int(cfg["vocab_size"]), eps=float(cfg.get("rms_norm_eps", 1e-5)),
+                      rope_theta=float(cfg.get("rope_theta", 10000.0)), rope_scaling=scaling)
+
+
+def checkpoint_weights(w: dict, s: ModelShape, device: str = "cuda") -> dict:
+    """Decode-model weights from a loaded checkpoint (nve_amd.loader.load_safetensors_w4:
+    block projections as GpuW4, every other tensor as stored), Hugging Face Llama names:
+    model.layers.{i}.{input_layernorm, post_attention_layernorm}.weight,
+    model.layers.{i}.self_attn.{q,k,v,o}_proj.weight, model.layers.{i}.mlp.{gate,up,down}_proj.weight,
+    model.norm.weight, model.embed_tokens.weight and lm_head.weight (absent: tied to the
+    embeddings).  Norms and embeddings become bf16; the lm_head is quantized to W4 on
+    the device (the decode head's GEMV is W4A8 / W4A16).  AWQ-scaled projections are
+    refused: the decode layer's GEMVs take no awq vector."""
+    from .gpu_layer import GpuW4
+
+    H, D = s.hidden, s.head_dim
+    QD, KD, F = s.heads * D, s.kv_heads * D, s.ffn
+    dims = {"q": (QD, H), "k": (KD, H), "v": (KD, H), "o": (H, QD), "gate": (F, H), "up": (F, H), "down": (H, F)}
+    src = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj", "o": "self_attn.o_proj",
+           "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+
+    def get(name):
+        if name not in w:
+            raise KeyError(f"checkpoint has no tensor {name}")
+        return w[name]
+
+    def bf16(t, shape):
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"shape {tuple(t.shape)}, expected {tuple(shape)}")
+        return t.to(device=device, dtype=torch.bfloat16).contiguous()
+
+    def w4(name, n, k):
+        g = get(name)
+        if not isinstance(g, GpuW4):
+            raise ValueError(f"{name} was not quantized on load")
+        if (g.n, g.k) != (n, k):
+            raise ValueError(f"{name}: [{g.n}, {g.k}], expected [{n}, {k}]")
+        if g.awq_scales is not None:
+            raise ValueError(f"{name}: AWQ-scaled weights are not supported by the decode layer")
+        return g.nibbles, g.scales
+
+    layers = []
+    for i in range(s.layers):
+        p = f"model.layers.{i}."
+        lw = {"input_norm": bf16(get(p + "input_layernorm.weight"), (H,)),
+              "post_attn_norm": bf16(get(p + "post_attention_layernorm.weight"), (H,))}
+        for nm, (n, k) in dims.items():
+            lw[nm] = w4(p + src[nm] + ".weight", n, k)
+        layers.append(lw)
+    embed = bf16(get("model.embed_tokens.weight"), (s.vocab, H))
+    head = w.get("lm_head.weight", embed)
+    if isinstance(head, GpuW4):
+        lm_head = w4("lm_head.weight", s.vocab, H)
+    else:
+        g = GpuW4.quantize(bf16(head, (s.vocab, H)))
+        lm_head = (g.nibbles, g.scales)
+    return {"layers": layers, "final_norm": bf16(get("model.norm.weight"), (H,)), "lm_head": lm_head,
+            "embed": embed}
+
+
 class DecodeModel:
     """Device-resident synthetic decoder; weights and caches are torch tensors (plumbing),
     every computation runs in libnve_hip.so."""
 
     def __init__(self, shape: ModelShape = LLAMA_3_2_3B, *, max_seq: int = 1024, prefill: int = 512,
                  w4a16_frac: float = 0.3, seed: int = 0x4E5645, lm_head_w4a8: bool = True,
-                 importance: np.ndarray | None = None, device: str = "cuda"):
+                 importance: np.ndarray | None = None, device: str = "cuda", weights: dict | None = None):
+        """weights: None for seeded random weights, or a checkpoint loaded with
+        nve_amd.loader.load_safetensors_w4 (Hugging Face Llama tensor names; see
+        checkpoint_weights).  `prefill` cached positions hold seeded N(0, 1) keys and
+        values either way (0 for an empty cache)."""
         assert prefill < max_seq
         self.shape = s = shape
         self.max_seq = max_seq
@@ -110,11 +192,15 @@ class DecodeModel:
         def norm_w(n):
             return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
 
+        loaded = checkpoint_weights(weights, s, device) if weights is not None else None
         self.layers = []
-        for _ in range(s.layers):
-            lw = {"input_norm": norm_w(H), "post_attn_norm": norm_w(H),
-                  "q": qw(QD, H), "k": qw(KD, H), "v": qw(KD, H), "o": qw(H, QD),
-                  "gate": qw(F, H), "up": qw(F, H), "down": qw(H, F)}
+        for li in range(s.layers):
+            if loaded is not None:
+                lw = dict(loaded["layers"][li])
+            else:
+                lw = {"input_norm": norm_w(H), "post_attn_norm": norm_w(H),
+                      "q": qw(QD, H), "k": qw(KD, H), "v": qw(KD, H), "o": qw(H, QD),
+                      "gate": qw(F, H), "up": qw(F, H), "down": qw(H, F)}
             kc = torch.zeros((s.kv_heads, max_seq, D), dtype=torch.bfloat16, device=device)
             vc = torch.zeros_like(kc)
             if prefill:
@@ -122,9 +208,12 @@ class DecodeModel:
                 vc[:, :prefill].copy_(torch.randn((s.kv_heads, prefill, D), generator=g, device=device))
             lw["k_cache"], lw["v_cache"] = kc, vc
             self.layers.append(lw)
-        self.final_norm = norm_w(H)
-        self.lm_head = qw(s.vocab, H)
-        self.embed = torch.randn((s.vocab, H), generator=g, device=device).to(torch.bfloat16)
+        if loaded is not None:
+            self.final_norm, self.lm_head, self.embed = loaded["final_norm"], loaded["lm_head"], loaded["embed"]
+        else:
+            self.final_norm = norm_w(H)
+            self.lm_head = qw(s.vocab, H)
+            self.embed = torch.randn((s.vocab, H), generator=g, device=device).to(torch.bfloat16)
         cos, sin = rope_tables(D, max_seq, s.rope_theta, s.rope_scaling)
         self.rope_cos = torch.from_numpy(cos).to(device)
         self.rope_sin = torch.from_numpy(sin).to(device)

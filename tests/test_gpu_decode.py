@@ -181,3 +181,70 @@ def test_decode_long_cache(torch_dev, split, monkeypatch):
     monkeypatch.setenv("NVE_ATTN_SPLIT", split)
     m = _model(torch_dev, 4, 2, 64, layers=2, importance=(0.0, 1.0), max_seq=8256, prefill=8190)
     _run_teacher_forced(torch_dev, m, steps=3)
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_decode_from_checkpoint(torch_dev, tmp_path, tied):
+    """A Hugging Face Llama checkpoint (config.json + safetensors, bf16) loaded with
+    load_safetensors_w4 drives the decode step: projections are the on-load Q4_0 of the
+    stored matrices, norms and embeddings the stored bf16, the lm_head the Q4_0 of
+    lm_head.weight or, tied, of the embeddings; the step matches the oracle."""
+    import json
+    from safetensors.torch import save_file
+    from nve_amd import hip_kernels as hk
+    from nve_amd.decode import DecodeModel, shape_from_hf_config
+    from nve_amd.loader import load_safetensors_w4
+
+    torch = torch_dev
+    cfg = {"hidden_size": 256, "num_hidden_layers": 2, "num_attention_heads": 4, "num_key_value_heads": 2,
+           "intermediate_size": 512, "vocab_size": 384, "rms_norm_eps": 1e-5, "rope_theta": 500000.0,
+           "rope_scaling": {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                            "high_freq_factor": 4.0, "original_max_position_embeddings": 64}}
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    s = shape_from_hf_config(json.loads((tmp_path / "config.json").read_text()))
+    assert (s.head_dim, s.kv_heads, s.rope_scaling.factor) == (64, 2, 8.0)
+    g = torch.Generator().manual_seed(3)
+    H, F, QD, KD = s.hidden, s.ffn, s.heads * s.head_dim, s.kv_heads * s.head_dim
+
+    def mat(n, k):
+        return (torch.randn((n, k), generator=g) * 0.05).to(torch.bfloat16)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16)
+
+    t = {"model.embed_tokens.weight": mat(s.vocab, H), "model.norm.weight": norm(H)}
+    for i in range(s.layers):
+        p = f"model.layers.{i}."
+        t.update({p + "input_layernorm.weight": norm(H), p + "post_attention_layernorm.weight": norm(H),
+                  p + "self_attn.q_proj.weight": mat(QD, H), p + "self_attn.k_proj.weight": mat(KD, H),
+                  p + "self_attn.v_proj.weight": mat(KD, H), p + "self_attn.o_proj.weight": mat(H, QD),
+                  p + "mlp.gate_proj.weight": mat(F, H), p + "mlp.up_proj.weight": mat(F, H),
+                  p + "mlp.down_proj.weight": mat(H, F)})
+    if not tied:
+        t["lm_head.weight"] = mat(s.vocab, H)
+    # two shards, as large checkpoints come
+    names = sorted(t)
+    save_file({n: t[n] for n in names[::2]}, str(tmp_path / "model-00001.safetensors"))
+    save_file({n: t[n] for n in names[1::2]}, str(tmp_path / "model-00002.safetensors"))
+    w = load_safetensors_w4([tmp_path / "model-00001.safetensors", tmp_path / "model-00002.safetensors"])
+    m = DecodeModel(s, max_seq=48, prefill=20, importance=np.array([0.0, 1.0]), weights=w)
+
+    nib, sc = hk.q4_quantize(t["model.layers.1.mlp.down_proj.weight"].cuda())
+    assert torch.equal(m.layers[1]["down"][0], nib) and torch.equal(m.layers[1]["down"][1], sc)
+    assert torch.equal(m.layers[0]["input_norm"].cpu(), t["model.layers.0.input_layernorm.weight"])
+    assert torch.equal(m.embed.cpu(), t["model.embed_tokens.weight"])
+    head = t["model.embed_tokens.weight" if tied else "lm_head.weight"]
+    nib, sc = hk.q4_quantize(head.cuda())
+    assert torch.equal(m.lm_head[0], nib) and torch.equal(m.lm_head[1], sc)
+    _run_teacher_forced(torch, m, steps=3)
+
+
+def test_decode_checkpoint_rejects_mismatch(torch_dev):
+    from nve_amd.decode import ModelShape, checkpoint_weights
+    s = ModelShape(hidden=64, layers=1, heads=2, kv_heads=1, head_dim=32, ffn=128, vocab=64)
+    with pytest.raises(KeyError):
+        checkpoint_weights({}, s)
+    w = {"model.layers.0.input_layernorm.weight": torch_dev.ones(64),
+         "model.layers.0.post_attention_layernorm.weight": torch_dev.ones(32)}
+    with pytest.raises(ValueError):
+        checkpoint_weights(w, s)

@@ -57,3 +57,23 @@ def test_q4_block_file_errors(tmp_path):
     read_q4_blocks(str(path), 2, 64)      # 80 bytes: fits
     with pytest.raises(ValueError):
         read_q4_blocks(str(path), 2, 64, offset=40)
+
+
+def test_shape_from_hf_config():
+    """config.json fields -> ModelShape (the fields src/config.rs reads)."""
+    from nve_amd.decode import ModelShape, shape_from_hf_config
+    cfg = {"hidden_size": 3072, "num_hidden_layers": 28, "num_attention_heads": 24, "num_key_value_heads": 8,
+           "intermediate_size": 8192, "vocab_size": 128256, "rms_norm_eps": 1e-5, "rope_theta": 500000.0,
+           "rope_scaling": {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                            "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}}
+    s = shape_from_hf_config(cfg)
+    assert (s.hidden, s.layers, s.heads, s.kv_heads, s.head_dim, s.ffn, s.vocab) == \
+        (3072, 28, 24, 8, 128, 8192, 128256)
+    assert s.rope_scaling.factor == 32.0 and s.rope_scaling.original_max_position_embeddings == 8192
+    # head_dim given explicitly wins; no kv heads means multi-head attention; no scaling
+    s = shape_from_hf_config({"hidden_size": 256, "num_hidden_layers": 2, "num_attention_heads": 2,
+                              "head_dim": 64, "intermediate_size": 512, "vocab_size": 100})
+    assert (s.head_dim, s.kv_heads, s.rope_scaling, s.rope_theta, s.eps) == (64, 2, None, 10000.0, 1e-5)
+    assert isinstance(s, ModelShape)
+    with pytest.raises(ValueError):
+        shape_from_hf_config({**cfg, "rope_scaling": {"rope_type": "yarn", "factor": 4.0}})
