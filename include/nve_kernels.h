@@ -226,8 +226,9 @@ int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles
  * F32 or x's dtype, the weights are dequantized into the workspace (nve_hip_dequant_w4,
  * bit-identical to the reference dequant) and multiplied by hipBLASLt (fp32
  * accumulation); otherwise it runs nve_hip_gemm_w4a16.  The first call per device and
- * shape creates the hipBLASLt handle and selects the algorithm, so make it outside
- * graph capture.  No counterpart in the reference's FFI (it makes two calls). */
+ * shape creates the hipBLASLt handle and selects the algorithm; made under graph
+ * capture, such a call runs nve_hip_gemm_w4a16 instead, so make it once before
+ * capturing.  No counterpart in the reference's FFI (it makes two calls). */
 size_t nve_hip_gemm_w4a16_workspace_bytes(int M, int N, int K);
 int nve_hip_gemm_w4a16_ws(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,
                           const float *awq, void *out, int out_dtype, int N, int K, void *workspace,

@@ -75,7 +75,8 @@ size_t gemm_w4a16_ws_bytes(int M, int N, int K) {
 // Dequant + hipBLASLt when M >= kGemmBlasMinM, the workspace is large enough and the
 // output is F32 or x's dtype; otherwise the fused kernel.  The first call per device and
 // shape creates the hipBLASLt handle and picks the fastest of up to kBlasCandidates
-// heuristic algorithms by timing them on the caller's stream (not under graph capture).
+// heuristic algorithms by timing them on the caller's stream; under graph capture a
+// device or shape without that state takes the fused kernel instead.
 hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
                                 const float* awq, void* out, int out_dt, int N, int K, void* ws, size_t ws_bytes,
                                 hipStream_t s) {
@@ -85,6 +86,10 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) return e;
+  const bool capturing = cap != hipStreamCaptureStatusNone;
   hipblasLtHandle_t h = nullptr;
   hipblasLtMatmulAlgo_t algo;
   Descs ds;
@@ -92,13 +97,17 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
   {
     std::lock_guard<std::mutex> lk(g_mu);
     auto hi = g_handles.find(dev);
+    const auto key = std::make_tuple(dev, M, N, K, x_dt, out_dt);
+    // Handle creation and the first call's timing (event synchronisation) cannot run
+    // under graph capture: an unseen device or shape is served by the fused kernel.
+    if (capturing && (hi == g_handles.end() || g_algo.find(key) == g_algo.end()))
+      return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
     if (hi == g_handles.end()) {
       if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotSupported;
       g_handles[dev] = h;
     } else {
       h = hi->second;
     }
-    const auto key = std::make_tuple(dev, M, N, K, x_dt, out_dt);
     auto ai = g_algo.find(key);
     if (ai == g_algo.end()) {
       hipblasLtMatmulPreference_t pref = nullptr;

@@ -172,3 +172,34 @@ def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
         a = hk.gemm_w4a16(x, nib, sc, n, k, out_dtype=torch.float16).cpu()
         b = hk.gemm_w4a16_ws(x, nib, sc, n, k, None, out_dtype=torch.float16).cpu()
         assert torch.equal(a, b), m
+
+
+def test_gemm_w4a16_ws_graph_capture(orc, torch_dev, hk):
+    """Under HIP graph capture: a shape first seen during capture takes the fused kernel
+    (no handle creation or timing in the graph); after an eager call has selected the
+    algorithm, the captured graph replays the BLAS path.  Every replay matches eager."""
+    torch = torch_dev
+    n, k = 512, 1024
+    data = orc.q4_from_f32(weights(n, k, seed=9, std=0.05))
+    nib, sc = (torch.from_numpy(a).cuda() for a in orc.extract_for_gpu(data, n, k))
+    for m, warm in ((520, False), (640, True)):
+        print(f"gemm_ws capture m={m} warm={warm}", flush=True)
+        x = torch.randn((m, k), device="cuda").to(torch.float16)
+        ws = torch.empty(hk.gemm_w4a16_workspace_bytes(m, n, k), dtype=torch.uint8, device="cuda")
+        out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+        eager_fused = hk.gemm_w4a16(x, nib, sc, n, k, out_dtype=torch.float16)
+        if warm:
+            eager = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out.copy_(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16))
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            if warm:
+                assert torch.equal(out, eager)
+            else:
+                assert torch.equal(out, eager_fused)
