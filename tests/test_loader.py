@@ -77,3 +77,21 @@ def test_shape_from_hf_config():
     assert isinstance(s, ModelShape)
     with pytest.raises(ValueError):
         shape_from_hf_config({**cfg, "rope_scaling": {"rope_type": "yarn", "factor": 4.0}})
+
+
+def test_checkpoint_weights_rejects_mismatch():
+    """A missing tensor is a KeyError; a norm, embedding or projection whose shape does
+    not match the config, or a projection that was not quantized on load, a ValueError."""
+    import torch
+    from nve_amd.decode import ModelShape, checkpoint_weights
+    s = ModelShape(hidden=64, layers=1, heads=2, kv_heads=1, head_dim=32, ffn=128, vocab=64)
+    with pytest.raises(KeyError):
+        checkpoint_weights({}, s, device="cpu")
+    p = "model.layers.0."
+    w = {p + "input_layernorm.weight": torch.ones(64), p + "post_attention_layernorm.weight": torch.ones(32)}
+    with pytest.raises(ValueError):
+        checkpoint_weights(w, s, device="cpu")
+    w[p + "post_attention_layernorm.weight"] = torch.ones(64)
+    w[p + "self_attn.q_proj.weight"] = torch.ones(64, 64)  # stored dense: not quantized on load
+    with pytest.raises(ValueError):
+        checkpoint_weights(w, s, device="cpu")
