@@ -636,6 +636,9 @@ def main():
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--cpu-decode-tokens", type=int, default=3)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-prefill", type=int, default=512,
+                    help="cached positions before the timed tokens (--decode-only)")
+    ap.add_argument("--decode-max-seq", type=int, default=1024, help="KV cache slots (--decode-only)")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the 3B decode measurement (for profiling; no bench line)")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -666,7 +669,8 @@ def main():
         batched_probe(torch, L, hk)
         return
     if args.decode_only:
-        print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True)}))
+        print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True,
+                                                 prefill=args.decode_prefill, max_seq=args.decode_max_seq)}))
         return
 
     # weight copies: layer set 136 MB -> 8 copies (1.09 GB); lm_head 328 MB -> 4 copies
