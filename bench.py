@@ -20,12 +20,17 @@ value = algorithmic bytes of one step / measured step time (GB/s), with the
 algorithmic bytes of a GEMV = N*K/2 (nibbles) + N*K/32*4 (f32 scales) + activation
 bytes (W4A8: K + K/32*4, W4A16: 2K) + output bytes.
 
-The roofline object reports the dominant kernel of the step (the W4A8 GEMV at the
-lm_head shape, fp32 logits: the largest single launch; it is the only launch of its
-kernel instantiation in the step) timed on its own in a graph of back-to-back
-launches with HIP events on the stream it runs on.  cpu_baseline times the
-reference's CPU quantized GEMV (QuantizedTensor::matvec_f32 + q4_dot_row_avx2,
-restated in oracle/) on the host cores over a bounded sample.
+The roofline object reports the dominant kernel of the step: the lm_head launches
+(128256x4096, fp32 logits), which take more than half of the step.  Both lm_head
+launches of the step are timed with the step's own entry points and arguments (so the
+same kernel instantiations: the W4A8 GEMV that quantizes its fp16 input in-kernel,
+nve_hip_matvec_w4a8_x, and the W4A16 GEMV on bf16 activations), each on its own in a
+graph of back-to-back launches over rotating weight copies, with HIP events on the
+stream the graph is replayed on; `roofline` is the slower of the two and
+`roofline_other` the other.  cpu_baseline times the reference's CPU quantized GEMV
+(QuantizedTensor::matvec_f32 + q4_dot_row_avx2, restated in oracle/) on every host
+core this process may run on (os.sched_getaffinity, as rayon's default pool) over a
+bounded sample.
 
 Also in the line (measured beside the step, not part of `value`): every suite shape
 timed on its own (graphs of 40 back-to-back launches over 8 weight copies; GB/s and
@@ -331,6 +336,33 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40, suite=SU
     return rows
 
 
+def step_head_kernels(torch, step, launches_per_graph: int = 20) -> dict:
+    """The step's two lm_head launches, each with the step's own entry point and
+    arguments (same kernel instantiation as in the timed step), timed on their own: a
+    graph of back-to-back launches over the rotating lm_head copies, HIP events on the
+    stream the graph is replayed on."""
+    n, k = 128256, 4096
+    copies = len(step.w["lm_head"])
+    res = {}
+    for label, fn in (("w4a8_x", lambda ci, s: step.w4a8_x("lm_head", ci, step.acts["final16"], s)),
+                      ("w4a16", lambda ci, s: step.w4a16("lm_head", ci, step.acts["finalb"], s))):
+        def body(fn=fn):
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(launches_per_graph):
+                fn(i % copies, s)
+        body()
+        g = capture(torch, body)
+        time_graphs(torch, [g], 2)
+        us = time_graphs(torch, [g], 5) * 1e3 / launches_per_graph
+        prec = "w4a8" if label == "w4a8_x" else "w4a16"
+        b = gemv_bytes(n, k, prec, 4)
+        if label == "w4a8_x":
+            b += 2 * k - (k + (k // 32) * 4)  # reads the fp16 vector instead of int8 + scales
+        res[label] = {"us": round(us, 3), "bytes": b, "GBs": round(b / us / 1e3, 1)}
+        log(f"  step lm_head {label:7s} {us:8.2f} us {b / us / 1e3:8.1f} GB/s")
+    return res
+
+
 def batched_sweep(torch, L, weights, launches_per_graph: int = 40):
     """W4A8 at M in {1,2,4,8,16} activation rows (per-row absmax
     int8, bf16 scales) on the 8B gate (14336x4096) and down (4096x14336) shapes.
@@ -393,12 +425,35 @@ def buf_gbs(nbytes, ms):
     return nbytes / (ms * 1e-3) / 1e9
 
 
+def host_cpus() -> tuple[int, str, str | None]:
+    """(threads to use = every core this process may run on, CPU model string, the
+    cgroup CPU quota if one is set)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    quota = None
+    try:
+        q = open("/sys/fs/cgroup/cpu.max").read().split()
+        if q and q[0] != "max":
+            quota = f"{int(q[0]) / int(q[1]):.1f} CPUs"
+    except (OSError, ValueError, IndexError):
+        pass
+    return n, model, quota
+
+
 def cpu_baseline(target_s: float = 12.0) -> dict:
     """The reference's CPU quantized GEMV (q4_dot_row_avx2 + row-parallel matvec_f32,
-    restated in oracle/) over 8B gate_proj + down_proj, on the host cores."""
+    restated in oracle/) over 8B gate_proj + down_proj, on every host core this
+    process may use (rayon's default pool, src/quantize.rs:476)."""
     import numpy as np
     from oracle import oracle as orc
-    threads = min(16, os.cpu_count() or 1)
+    threads, model, quota = host_cpus()
     r = np.random.default_rng(7)
     mats = []
     for n, k in ((14336, 4096), (4096, 14336)):
@@ -418,7 +473,8 @@ def cpu_baseline(target_s: float = 12.0) -> dict:
         if el >= target_s:
             break
     gbs = b * reps / el / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port", "cpu_model": model,
+            "cgroup_cpu_quota": quota,
             "sample": f"8B gate_proj 14336x4096 + down_proj 4096x14336, W4 x f32 (QuantizedTensor::matvec_f32 / "
                       f"q4_dot_row_avx2 restated in oracle/oracle.c), {reps} passes in {el:.1f} s, "
                       f"{threads} threads; GB/s over the same algorithmic bytes as the GPU"}
@@ -447,7 +503,10 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
     the long-context line, GPU only)."""
     from nve_amd.decode import LLAMA_3_2_3B, DecodeModel
     s = LLAMA_3_2_3B
+    if prefill + warm + 1 >= max_seq:
+        raise SystemExit(f"decode: prefill ({prefill}) + warm-up ({warm}) + 1 must be below max_seq ({max_seq})")
     tokens = min(tokens, max_seq - prefill - warm - 1)
+    assert tokens >= 1
     m = DecodeModel(s, max_seq=max_seq, prefill=prefill)
     m.capture()
     m.start(1)
@@ -480,7 +539,7 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
         from oracle import decode_ref as dr
         log("decode 3B CPU leg: copying weights to host")
         hm = dr.HostModel(m, with_cpu_blocks=True)
-        threads = min(16, os.cpu_count() or 1)
+        threads, model, quota = host_cpus()
         h = hm.embed[1].copy()
         h, _ = dr.reference_step(hm, h, prefill, threads)  # warm
         t0 = time.perf_counter()
@@ -488,6 +547,7 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
             h, _ = dr.reference_step(hm, h, prefill + 1 + i, threads)
         el = time.perf_counter() - t0
         rec["cpu_baseline"] = {"value": round(cpu_tokens / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+                               "cpu_model": model, "cgroup_cpu_quota": quota,
                                "sample": f"{cpu_tokens} greedy tokens (after 1 warm) of the same 3B model on the "
                                          f"reference CPU decode path (QuantizedTensor::matvec_f32 / q4_dot_row_avx2 "
                                          f"restated in oracle/, f32 activations), {el:.1f} s"}
@@ -596,9 +656,10 @@ def batched_probe(torch, L, hk):
 
 def traffic_probe(torch, L, hk):
     """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
-    256 MiB (calibration: 256 MiB read + 256 MiB written), then 5 launches of the
-    roofline kernel (W4A8 GEMV, lm_head 128256x4096, fp32 logits) on 5 distinct weight
-    copies.  Prints the launch order so per-dispatch counters can be matched."""
+    256 MiB (calibration: 256 MiB read + 256 MiB written), then the step's two lm_head
+    launches (128256x4096, fp32 logits) 5 times each on 5 distinct weight copies: W4A8
+    quantizing its fp16 input in-kernel (nve_hip_matvec_w4a8_x), then W4A16 on bf16
+    activations.  Prints the launch order so per-dispatch counters can be matched."""
     g = torch.Generator(device="cuda").manual_seed(11)
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
@@ -614,16 +675,23 @@ def traffic_probe(torch, L, hk):
         w = torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
         sets.append(hk.q4_quantize(w))
         del w
-    x16 = make_activation(torch, k, 5).to(torch.float16)
-    xq, xs = hk.quantize_f16_q8(x16)
+    x = make_activation(torch, k, 5)
+    x16, xb = x.to(torch.float16), x.to(torch.bfloat16)
     out = torch.empty(n, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
+    s = torch.cuda.current_stream().cuda_stream
     for nib, sc in sets:
-        assert L.nve_hip_matvec_w4a8(xq.data_ptr(), xs.data_ptr(), nib.data_ptr(), sc.data_ptr(), out.data_ptr(),
-                                     2, n, k, torch.cuda.current_stream().cuda_stream) == 0
+        assert L.nve_hip_matvec_w4a8_x(x16.data_ptr(), 0, nib.data_ptr(), sc.data_ptr(), out.data_ptr(), 2, n, k,
+                                       s) == 0
+    for nib, sc in sets:
+        assert L.nve_hip_matvec_w4a16(xb.data_ptr(), 1, nib.data_ptr(), sc.data_ptr(), None, out.data_ptr(), 2, n, k,
+                                      s) == 0
     torch.cuda.synchronize()
-    print(json.dumps({"probe": "traffic", "copy_bytes": 256 << 20, "gemv_bytes_per_launch": gemv_bytes(n, k, "w4a8", 4),
-                      "gemv_launches": 5}), flush=True)
+    b8 = gemv_bytes(n, k, "w4a8", 4) + 2 * k - (k + (k // 32) * 4)
+    print(json.dumps({"probe": "traffic", "copy_bytes": 256 << 20,
+                      "launches": [{"label": "w4a8_x", "count": 5, "bytes": b8},
+                                   {"label": "w4a16", "count": 5, "bytes": gemv_bytes(n, k, "w4a16", 4)}]}),
+          flush=True)
 
 
 def main():
@@ -648,6 +716,8 @@ def main():
     ap.add_argument("--decode-traffic-probe", action="store_true",
                     help="6 eager (not graph-replayed) 3B decode steps for rocprofv3 --pmc (no bench line)")
     args = ap.parse_args()
+    if args.decode_prefill < 0 or args.decode_prefill + 16 + 1 >= args.decode_max_seq:
+        ap.error("--decode-prefill + 17 (16 warm-up tokens and one timed) must be below --decode-max-seq")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
@@ -694,9 +764,10 @@ def main():
     value = sb / (ms * 1e-3) / 1e9
     log(f"step: {ms * 1e3:.1f} us, {sb / 1e6:.1f} MB algorithmic, {value:.1f} GB/s")
 
+    log("the step's lm_head launches:")
+    heads = step_head_kernels(torch, step)
     log("per-kernel table:")
     table = kernel_table(torch, L, weights, acts)
-    head = table["lm_head/w4a8"]
     log("batched W4A8 sweep (per-token int8 activations):")
     sweep = batched_sweep(torch, L, weights)
     stream_gbs = stream_probe(torch, L)
@@ -732,16 +803,27 @@ def main():
     prefill = prefill_gemm(torch, hk)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
-    # HBM bytes per launch of the roofline kernel, from the calibrated rocprofv3
+    # HBM bytes per launch of the step's lm_head kernels, from the calibrated rocprofv3
     # FETCH_SIZE / WRITE_SIZE passes over `bench.py --traffic-probe` (recorded in
-    # profiles/w4a8_gemv_lm_head_8b_traffic.md)
-    traffic = None
-    tf = ROOT / "profiles" / "w4a8_gemv_lm_head_8b_traffic.md"
+    # profiles/lm_head_8b_step_kernels_traffic.md)
+    traffic = {}
+    tf = ROOT / "profiles" / "lm_head_8b_step_kernels_traffic.md"
     if tf.exists():
         import re
         m = re.search(r"```json\n(.*?)\n```", tf.read_text(), re.S)
         if m:
-            traffic = json.loads(m.group(1)).get("hbm_bytes_per_launch")
+            traffic = json.loads(m.group(1)).get("hbm_bytes_per_launch", {})
+    kernels = {"w4a8_x": "w4a8_gemv_kernel<F32, R=2, NJ=2, SRC_F16> (nve_hip_matvec_w4a8_x, lm_head 128256x4096, "
+                         "fp16 input quantized in-kernel, fp32 logits)",
+               "w4a16": "w4a16_gemv_kernel<bf16 x, F32 out> (nve_hip_matvec_w4a16, lm_head 128256x4096, fp32 logits)"}
+    order = sorted(heads, key=lambda kk: -heads[kk]["us"])
+
+    def roof(label):
+        h = heads[label]
+        return {"kernel": kernels[label], "bound": "hbm", "achieved": h["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(h["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic.get(label),
+                "achievable_peak": round(stream_gbs, 1), "frac_of_achievable": round(h["GBs"] / stream_gbs, 4),
+                "bytes_per_launch": h["bytes"], "us_per_launch": h["us"]}
 
     rec = {
         "metric": METRIC,
@@ -764,20 +846,8 @@ def main():
             "step_bytes": sb,
             "graph": "one HIP graph per weight copy, replayed round-robin",
         },
-        "roofline": {
-            "kernel": "w4a8_gemv_kernel (lm_head 128256x4096, fp32 logits)",
-            "bound": "hbm",
-            "achieved": head["GBs"],
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(head["GBs"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            # the second denominator: the in-repo streaming-read probe on this GPU
-            "achievable_peak": round(stream_gbs, 1),
-            "frac_of_achievable": round(head["GBs"] / stream_gbs, 4),
-            "bytes_per_launch": head["bytes"],
-            "us_per_launch": head["us"],
-        },
+        "roofline": roof(order[0]),
+        "roofline_other": roof(order[1]),
         "cpu_baseline": cpu,
         "suite_8b": table,
         "suite_8b_aggregate_GBs": {"w4a8_layers": agg("w4a8", layer_names), "w4a16_layers": agg("w4a16", layer_names),

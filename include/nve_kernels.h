@@ -16,8 +16,17 @@
  *     hipError_t from the launch, < 0 = an argument error below).  The drop-in
  *     `void` launchers with the reference's names call them, and on failure print
  *     one line to stderr and record the status for nve_hip_last_status().
- *   - Alignment: nibbles and int8 activations 16-byte aligned; scales 4-byte aligned;
- *     fp16/bf16 vectors 16-byte aligned.
+ *   - Alignment: the main kernels stream 16-byte words and want nibbles, int8
+ *     activations and fp16/bf16 vectors 16-byte aligned, scales and awq 4-byte aligned.
+ *     The reference's five launchers and their twins (nve_quantize_f16_q8 /
+ *     nve_hip_quantize_q8, nve_matvec_w4a8 / nve_hip_matvec_w4a8, nve_matvec_w4a16 /
+ *     nve_hip_matvec_w4a16, nve_qkv_matvec_w4a16 / nve_hip_qkv_matvec_w4a16 /
+ *     nve_hip_grouped_matvec_w4a16, nve_dequant_w4a16 / nve_hip_dequant_w4) also accept
+ *     the reference's own contract (cuda/nve_kernels.cu:789-794, 829-832, 330-433):
+ *     W4A8 nibbles 2-byte and xq 4-byte aligned, W4A16 / dequant nibbles at any byte,
+ *     16-bit vectors 2-byte, f32 vectors 4-byte aligned; such calls run kernels that
+ *     load at the reference's granularity (same results, lower bandwidth).  Below that
+ *     contract: NVE_ERR_ALIGN.  Every other entry point keeps the 16-byte rule.
  *   - Limits: K % 32 == 0, 32 <= K <= NVE_MAX_K, 1 <= N; M <= NVE_MAX_M.
  */
 #ifndef NVE_KERNELS_H
@@ -83,7 +92,7 @@ void nve_qkv_matvec_w4a16(const uint16_t *x, const uint8_t *q_nib, const float *
 
 /* Replaces nve_dequant_w4a16 (cuda/nve_kernels.cu:397-433; the prefill path's weight
  * expansion before a dense matmul).  out fp16 [N, K] = f16_rne(f32(nib - 8) * scale
- * [* awq[k]]); awq may be NULL.  out 16-byte aligned. */
+ * [* awq[k]]); awq may be NULL. */
 void nve_dequant_w4a16(const uint8_t *nibbles, const float *scales, const float *awq, uint16_t *out,
                        int N, int K, void *stream);
 

@@ -31,14 +31,17 @@ static bool dtype_ok(int dt) { return dt == NVE_DT_F16 || dt == NVE_DT_BF16 || d
 static bool out_ok(int dt) { return dtype_ok(dt) || dt == NVE_DT_F32_ACCUM; }
 static bool out_aligned(const void* p, int dt) { return aligned(p, dt >= NVE_DT_F32 ? 4 : 2); }
 
-// Common GEMV argument checks.
-static int check_gemv(const void* nib, const void* sc, const void* out, int N, int K) {
+// Common GEMV argument checks; nib_align = the nibble alignment the caller's path needs
+// (16 for the main kernels; 2 or 1 where the reference-contract kernels of
+// gemv_unaligned.hip can serve the call).
+static int check_gemv(const void* nib, const void* sc, const void* out, int N, int K, uintptr_t nib_align = 16) {
   if (!nib || !sc || !out) return NVE_ERR_NULL;
   if (N < 1 || K < 32 || K % 32 != 0) return NVE_ERR_SHAPE;
   if (K > NVE_MAX_K) return NVE_ERR_TOO_LARGE;
-  if (!aligned(nib, 16) || !aligned(sc, 4) || !aligned(out, 2)) return NVE_ERR_ALIGN;
+  if (!aligned(nib, nib_align) || !aligned(sc, 4) || !aligned(out, 2)) return NVE_ERR_ALIGN;
   return NVE_OK;
 }
+static uintptr_t dt_size(int dt) { return dt == NVE_DT_F32 ? 4 : 2; }
 
 static void report(const char* fn, int st) {
   if (st != NVE_OK) fprintf(stderr, "nve_hip: %s failed: %s (%d)\n", fn, nve_hip_status_string(st), st);
@@ -63,6 +66,14 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
 hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, float* scales,
                             hipStream_t stream);
 hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream);
+hipError_t launch_w4a8_unaligned(const int8_t* xq, const float* xs, const uint8_t* nib, const float* ws, void* out,
+                                 int out_dt, int N, int K, hipStream_t s);
+hipError_t launch_w4a16_unaligned(const void* x, int x_dt, const uint8_t* nib, const float* sc, const float* awq,
+                                  void* out, int out_dt, int N, int K, hipStream_t s);
+hipError_t launch_q8_group_unaligned(const void* x, int xdt, size_t total, int8_t* xq, float* scales,
+                                     hipStream_t s);
+hipError_t launch_dequant_w4_unaligned(const uint8_t* nib, const float* scales, const float* awq, void* out,
+                                       int out_dt, int N, int K, hipStream_t s);
 hipError_t launch_w4a8_batched(int M, const int8_t* xq, const void* xs, int xs_mode,
                                const uint8_t* nib, const float* ws, void* out, int out_dt, int N,
                                int K, hipStream_t stream);
@@ -95,8 +106,12 @@ int nve_hip_quantize_q8(const void* x, int x_dtype, int M, int K, int8_t* xq, fl
   if (!x || !xq || !scales) return set_status(NVE_ERR_NULL);
   if (!dtype_ok(x_dtype)) return set_status(NVE_ERR_DTYPE);
   if (M < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
-  if (!aligned(x, 16) || !aligned(xq, 4) || !aligned(scales, 4)) return set_status(NVE_ERR_ALIGN);
-  return from_hip(launch_q8_group(x, x_dtype, (size_t)M * K, xq, scales, (hipStream_t)stream));
+  if (!aligned(scales, 4)) return set_status(NVE_ERR_ALIGN);
+  if (aligned(x, 16) && aligned(xq, 4))
+    return from_hip(launch_q8_group(x, x_dtype, (size_t)M * K, xq, scales, (hipStream_t)stream));
+  // the reference's contract: x aligned to its element size, xq to a byte
+  if (!aligned(x, dt_size(x_dtype))) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_q8_group_unaligned(x, x_dtype, (size_t)M * K, xq, scales, (hipStream_t)stream));
 }
 
 int nve_hip_quantize_q8_rows(const void* x, int x_dtype, int M, int K, int8_t* xq,
@@ -113,10 +128,15 @@ int nve_hip_matvec_w4a8(const int8_t* xq, const float* xq_scales, const uint8_t*
                         const float* wt_scales, void* out, int out_dtype, int N, int K,
                         void* stream) {
   if (!xq || !xq_scales) return set_status(NVE_ERR_NULL);
-  int st = check_gemv(nibbles, wt_scales, out, N, K);
+  int st = check_gemv(nibbles, wt_scales, out, N, K, 2);
   if (st != NVE_OK) return set_status(st);
   if (!out_ok(out_dtype)) return set_status(NVE_ERR_DTYPE);
-  if (!aligned(xq, 16) || !aligned(xq_scales, 4) || !out_aligned(out, out_dtype)) return set_status(NVE_ERR_ALIGN);
+  if (!aligned(xq, 4) || !aligned(xq_scales, 4) || !out_aligned(out, out_dtype)) return set_status(NVE_ERR_ALIGN);
+  // nibbles 2-byte / xq 4-byte aligned (the reference's contract) but not 16: the
+  // reference-granularity kernel
+  if (!aligned(nibbles, 16) || !aligned(xq, 16))
+    return from_hip(launch_w4a8_unaligned(xq, xq_scales, nibbles, wt_scales, out, out_dtype, N, K,
+                                          (hipStream_t)stream));
   W4Segs s{};
   s.nseg = 1;
   s.nib[0] = nibbles;
@@ -219,12 +239,16 @@ int nve_hip_matvec_w4a8_batched(int M, const int8_t* xq, const void* xq_scales, 
 int nve_hip_matvec_w4a16(const void* x, int x_dtype, const uint8_t* nibbles, const float* scales,
                          const float* awq, void* out, int out_dtype, int N, int K, void* stream) {
   if (!x) return set_status(NVE_ERR_NULL);
-  int st = check_gemv(nibbles, scales, out, N, K);
+  int st = check_gemv(nibbles, scales, out, N, K, 1);
   if (st != NVE_OK) return set_status(st);
   if ((x_dtype != NVE_DT_F16 && x_dtype != NVE_DT_BF16) || !out_ok(out_dtype))
     return set_status(NVE_ERR_DTYPE);
-  if (!aligned(x, 16) || (awq && !aligned(awq, 16)) || !out_aligned(out, out_dtype))
-    return set_status(NVE_ERR_ALIGN);
+  if (!aligned(x, 2) || (awq && !aligned(awq, 4)) || !out_aligned(out, out_dtype)) return set_status(NVE_ERR_ALIGN);
+  // aligned only to the reference's contract (nibbles 1, x 2, awq 4 bytes): the
+  // reference-granularity kernel
+  if (!aligned(nibbles, 16) || !aligned(x, 16) || (awq && !aligned(awq, 16)))
+    return from_hip(launch_w4a16_unaligned(x, x_dtype, nibbles, scales, awq, out, out_dtype, N, K,
+                                           (hipStream_t)stream));
   W4Segs s{};
   s.nseg = 1;
   s.nib[0] = nibbles;
@@ -243,19 +267,28 @@ int nve_hip_grouped_matvec_w4a16(const void* x, int x_dtype, const nve_w4_mat* m
     return set_status(NVE_ERR_DTYPE);
   W4Segs s{};
   s.nseg = count;
+  bool fast = aligned(x, 16);
   for (int i = 0; i < count; ++i) {
-    int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K);
+    int st = check_gemv(mats[i].nibbles, mats[i].scales, mats[i].out, mats[i].n, K, 1);
     if (st != NVE_OK) return set_status(st);
-    if ((mats[i].awq && !aligned(mats[i].awq, 16)) || !out_aligned(mats[i].out, out_dtype))
+    if ((mats[i].awq && !aligned(mats[i].awq, 4)) || !out_aligned(mats[i].out, out_dtype))
       return set_status(NVE_ERR_ALIGN);
+    fast = fast && aligned(mats[i].nibbles, 16) && (!mats[i].awq || aligned(mats[i].awq, 16));
     s.nib[i] = mats[i].nibbles;
     s.sc[i] = mats[i].scales;
     s.awq[i] = mats[i].awq;
     s.out[i] = mats[i].out;
     s.n[i] = mats[i].n;
   }
-  if (!aligned(x, 16)) return set_status(NVE_ERR_ALIGN);
-  return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
+  if (!aligned(x, 2)) return set_status(NVE_ERR_ALIGN);
+  if (fast) return from_hip(launch_w4a16(x, x_dtype, s, out_dtype, K, (hipStream_t)stream));
+  // aligned only to the reference's contract: one reference-granularity launch per matrix
+  for (int i = 0; i < count; ++i) {
+    const hipError_t e = launch_w4a16_unaligned(x, x_dtype, s.nib[i], s.sc[i], s.awq[i], s.out[i], out_dtype, s.n[i],
+                                                K, (hipStream_t)stream);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  return set_status(NVE_OK);
 }
 
 int nve_hip_qkv_matvec_w4a16(const void* x, int x_dtype, const uint8_t* q_nib, const float* q_sc,
@@ -305,9 +338,12 @@ int nve_hip_dequant_w4(const uint8_t* nibbles, const float* scales, const float*
   if (!nibbles || !scales || !out) return set_status(NVE_ERR_NULL);
   if (out_dtype != NVE_DT_F16 && out_dtype != NVE_DT_BF16 && out_dtype != NVE_DT_F32) return set_status(NVE_ERR_DTYPE);
   if (N < 1 || K < 32 || K % 32 != 0) return set_status(NVE_ERR_SHAPE);
-  if (!aligned(nibbles, 16) || !aligned(scales, 4) || !aligned(out, 16) || (awq && !aligned(awq, 16)))
+  if (!aligned(scales, 4) || !aligned(out, dt_size(out_dtype)) || (awq && !aligned(awq, 4)))
     return set_status(NVE_ERR_ALIGN);
-  return from_hip(launch_dequant_w4(nibbles, scales, awq, out, out_dtype, N, K, (hipStream_t)stream));
+  if (aligned(nibbles, 16) && aligned(out, 16) && (!awq || aligned(awq, 16)))
+    return from_hip(launch_dequant_w4(nibbles, scales, awq, out, out_dtype, N, K, (hipStream_t)stream));
+  // aligned only to the reference's contract (nibbles 1 byte, out its element size)
+  return from_hip(launch_dequant_w4_unaligned(nibbles, scales, awq, out, out_dtype, N, K, (hipStream_t)stream));
 }
 
 int nve_hip_gemm_w4a16(const void* x, int x_dtype, int M, const uint8_t* nibbles, const float* scales,

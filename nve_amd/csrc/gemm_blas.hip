@@ -40,7 +40,13 @@ hipDataType blas_type(int nve_dt) {
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;                                     // per device
-std::map<std::tuple<int, int, int, int, int, int>, hipblasLtMatmulAlgo_t> g_algo;  // dev, M, N, K, x, out
+// Selected algorithm per (dev, M, N, K, x, out); ok == false marks a shape for which no
+// candidate ran (that shape is served by the fused kernel from then on).
+struct AlgoChoice {
+  bool ok;
+  hipblasLtMatmulAlgo_t algo;
+};
+std::map<std::tuple<int, int, int, int, int, int>, AlgoChoice> g_algo;
 
 struct Descs {
   hipblasLtMatmulDesc_t op = nullptr;
@@ -63,6 +69,65 @@ bool make_descs(Descs& ds, int M, int N, int K, int x_dt, int out_dt) {
          hipblasLtMatrixLayoutCreate(&ds.a, blas_type(x_dt), K, N, K) == HIPBLAS_STATUS_SUCCESS &&
          hipblasLtMatrixLayoutCreate(&ds.b, blas_type(x_dt), K, M, K) == HIPBLAS_STATUS_SUCCESS &&
          hipblasLtMatrixLayoutCreate(&ds.d, blas_type(out_dt), N, M, N) == HIPBLAS_STATUS_SUCCESS;
+}
+
+// Heuristic candidates for the shape, each timed (3 runs) on the caller's stream; only
+// a candidate in the success state, within the workspace limit, whose runs all
+// returned success can be chosen.  ok == false when none qualifies (or no candidate
+// exists).  A single candidate is still run once to check it.  `out` and the
+// dequantized-weight part of `ws` hold scratch until the caller's product overwrites
+// them.
+AlgoChoice select_algo(hipblasLtHandle_t h, const Descs& ds, const void* x, void* ws, void* out,
+                       const uint8_t* nib, const float* sc, const float* awq, int x_dt, int N, int K,
+                       hipStream_t s, hipError_t* err) {
+  *err = hipSuccess;
+  AlgoChoice none{false, {}};
+  hipblasLtMatmulPreference_t pref = nullptr;
+  const uint64_t wsz = kBlasWorkspace;
+  hipblasLtMatmulHeuristicResult_t res[kBlasCandidates];
+  int found = 0;
+  const bool ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz,
+                                                        sizeof wsz) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulAlgoGetHeuristic(h, ds.op, ds.a, ds.b, ds.d, ds.d, pref, kBlasCandidates, res,
+                                                  &found) == HIPBLAS_STATUS_SUCCESS &&
+                  found > 0;
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (!ok) return none;
+  *err = launch_dequant_w4(nib, sc, awq, ws, x_dt, N, K, s);
+  if (*err != hipSuccess) return none;
+  void* bws = (char*)ws + round256((size_t)N * K * 2);
+  const float alpha = 1.0f, beta = 0.0f;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return none;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    hipEventDestroy(e0);
+    return none;
+  }
+  int best = -1;
+  float best_ms = 1e30f;
+  for (int c = 0; c < found; ++c) {
+    if (res[c].state != HIPBLAS_STATUS_SUCCESS || res[c].workspaceSize > kBlasWorkspace) continue;
+    bool run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d, &res[c].algo,
+                                  bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+    hipEventRecord(e0, s);
+    for (int r = 0; run_ok && r < 3; ++r)
+      run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d, &res[c].algo,
+                               bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+    hipEventRecord(e1, s);
+    float ms = 1e30f;
+    const bool synced = hipEventSynchronize(e1) == hipSuccess;
+    run_ok = run_ok && synced && hipGetLastError() == hipSuccess;
+    if (run_ok) hipEventElapsedTime(&ms, e0, e1);
+    if (run_ok && (best < 0 || ms < best_ms)) {
+      best_ms = ms;
+      best = c;
+    }
+  }
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  if (best < 0) return none;
+  return AlgoChoice{true, res[best].algo};
 }
 
 }  // namespace
@@ -91,16 +156,20 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
   if (e != hipSuccess) return e;
   const bool capturing = cap != hipStreamCaptureStatusNone;
   hipblasLtHandle_t h = nullptr;
-  hipblasLtMatmulAlgo_t algo;
   Descs ds;
   if (!make_descs(ds, M, N, K, x_dt, out_dt)) return hipErrorNotSupported;
+  const auto key = std::make_tuple(dev, M, N, K, x_dt, out_dt);
+  bool known = false;
+  AlgoChoice choice{false, {}};
   {
     std::lock_guard<std::mutex> lk(g_mu);
     auto hi = g_handles.find(dev);
-    const auto key = std::make_tuple(dev, M, N, K, x_dt, out_dt);
+    auto ai = g_algo.find(key);
+    known = ai != g_algo.end();
+    if (known) choice = ai->second;
     // Handle creation and the first call's timing (event synchronisation) cannot run
     // under graph capture: an unseen device or shape is served by the fused kernel.
-    if (capturing && (hi == g_handles.end() || g_algo.find(key) == g_algo.end()))
+    if (capturing && (hi == g_handles.end() || !known))
       return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
     if (hi == g_handles.end()) {
       if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotSupported;
@@ -108,56 +177,17 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
     } else {
       h = hi->second;
     }
-    auto ai = g_algo.find(key);
-    if (ai == g_algo.end()) {
-      hipblasLtMatmulPreference_t pref = nullptr;
-      const uint64_t wsz = kBlasWorkspace;
-      hipblasLtMatmulHeuristicResult_t res[kBlasCandidates];
-      int found = 0;
-      const bool ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
-                      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz,
-                                                            sizeof wsz) == HIPBLAS_STATUS_SUCCESS &&
-                      hipblasLtMatmulAlgoGetHeuristic(h, ds.op, ds.a, ds.b, ds.d, ds.d, pref, kBlasCandidates, res,
-                                                      &found) == HIPBLAS_STATUS_SUCCESS &&
-                      found > 0;
-      if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-      // no algorithm for this shape: the fused kernel serves it
-      if (!ok) return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
-      int best = 0;
-      if (found > 1) {
-        // first call for this shape: time the candidates on the caller's stream (the
-        // product is recomputed below, so `out` only holds scratch until then)
-        e = launch_dequant_w4(nib, sc, awq, ws, x_dt, N, K, s);
-        if (e != hipSuccess) return e;
-        void* bws = (char*)ws + round256((size_t)N * K * 2);
-        const float alpha = 1.0f, beta = 0.0f;
-        hipEvent_t e0, e1;
-        if (hipEventCreate(&e0) != hipSuccess) return hipErrorNotSupported;
-        if (hipEventCreate(&e1) != hipSuccess) { hipEventDestroy(e0); return hipErrorNotSupported; }
-        float best_ms = 1e30f;
-        for (int c = 0; c < found; ++c) {
-          if (res[c].state != HIPBLAS_STATUS_SUCCESS || res[c].workspaceSize > kBlasWorkspace) continue;
-          bool run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d,
-                                        &res[c].algo, bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
-          hipEventRecord(e0, s);
-          for (int r = 0; run_ok && r < 3; ++r)
-            run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d,
-                                     &res[c].algo, bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
-          hipEventRecord(e1, s);
-          float ms = 1e30f;
-          if (hipEventSynchronize(e1) == hipSuccess && run_ok) hipEventElapsedTime(&ms, e0, e1);
-          if (run_ok && ms < best_ms) {
-            best_ms = ms;
-            best = c;
-          }
-        }
-        hipEventDestroy(e0);
-        hipEventDestroy(e1);
-      }
-      ai = g_algo.emplace(key, res[best].algo).first;
-    }
-    algo = ai->second;
   }
+  if (!known) {
+    // First call for this shape: pick an algorithm outside the lock (two threads that
+    // race here both time the candidates; the first result stored is kept).
+    choice = select_algo(h, ds, x, ws, out, nib, sc, awq, x_dt, N, K, s, &e);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(g_mu);
+    choice = g_algo.emplace(key, choice).first->second;
+  }
+  if (!choice.ok) return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
+  const hipblasLtMatmulAlgo_t algo = choice.algo;
   void* wdq = ws;
   void* blas_ws = (char*)ws + round256((size_t)N * K * 2);
   e = launch_dequant_w4(nib, sc, awq, wdq, x_dt, N, K, s);

@@ -85,14 +85,19 @@ def _w4(t: tuple[torch.Tensor, torch.Tensor], n: int, k: int) -> W4Weight:
 
 def shape_from_hf_config(cfg: dict) -> ModelShape:
     """ModelShape from a Hugging Face Llama config.json dict (the fields the reference's
-    src/config.rs reads: hidden_size, num_hidden_layers, num_attention_heads,
-    num_key_value_heads, head_dim, intermediate_size, vocab_size, rms_norm_eps,
-    rope_theta, rope_scaling with rope_type "llama3")."""
+    generic loader reads from a checkpoint's config, src/arch.rs:200-262:
+    hidden_size, num_hidden_layers, num_attention_heads, num_key_value_heads, head_dim,
+    intermediate_size, vocab_size, rms_norm_eps, rope_theta -- default 10000 as at
+    src/arch.rs:221 -- and rope_scaling with rope_type "llama3"; rope_type "default"
+    means no scaling)."""
     heads = int(cfg["num_attention_heads"])
     hidden = int(cfg["hidden_size"])
     rs = cfg.get("rope_scaling") or None
     scaling = None
-    if rs and rs.get("rope_type", rs.get("type")) == "llama3":
+    rtype = rs.get("rope_type", rs.get("type")) if rs else None
+    if rtype == "default":
+        rs = None
+    if rs and rtype == "llama3":
         scaling = RopeScaling(float(rs["factor"]), float(rs.get("low_freq_factor", 1.0)),
                               float(rs.get("high_freq_factor", 4.0)),
                               int(rs.get("original_max_position_embeddings", 8192)))
@@ -105,13 +110,14 @@ def shape_from_hf_config(cfg: dict) -> ModelShape:
                       rope_theta=float(cfg.get("rope_theta", 10000.0)), rope_scaling=scaling)
 
 
-def checkpoint_weights(w: dict, s: ModelShape, device: str = "cuda") -> dict:
+def checkpoint_weights(w: dict, s: ModelShape, device: str = "cuda", tie_word_embeddings: bool = True) -> dict:
     """Decode-model weights from a loaded checkpoint (nve_amd.loader.load_safetensors_w4:
     block projections as GpuW4, every other tensor as stored), Hugging Face Llama names:
     model.layers.{i}.{input_layernorm, post_attention_layernorm}.weight,
     model.layers.{i}.self_attn.{q,k,v,o}_proj.weight, model.layers.{i}.mlp.{gate,up,down}_proj.weight,
     model.norm.weight, model.embed_tokens.weight and lm_head.weight (absent: tied to the
-    embeddings).  Norms and embeddings become bf16; the lm_head is quantized to W4 on
+    embeddings when tie_word_embeddings -- config.json's field of that name -- is true,
+    a KeyError otherwise).  Norms and embeddings become bf16; the lm_head is quantized to W4 on
     the device (the decode head's GEMV is W4A8 / W4A16).  AWQ-scaled projections are
     refused: the decode layer's GEMVs take no awq vector."""
     from .gpu_layer import GpuW4
@@ -151,6 +157,8 @@ def checkpoint_weights(w: dict, s: ModelShape, device: str = "cuda") -> dict:
             lw[nm] = w4(p + src[nm] + ".weight", n, k)
         layers.append(lw)
     embed = bf16(get("model.embed_tokens.weight"), (s.vocab, H))
+    if "lm_head.weight" not in w and not tie_word_embeddings:
+        raise KeyError("checkpoint has no tensor lm_head.weight and tie_word_embeddings is false")
     head = w.get("lm_head.weight", embed)
     if isinstance(head, GpuW4):
         lm_head = w4("lm_head.weight", s.vocab, H)

@@ -58,8 +58,10 @@ def test_w4a8_argument_errors(L):
     assert f(P16, P16, P16, P16, P16, 2, 8, 48, None) == -2            # K % 32
     assert f(P16, P16, P16, P16, P16, 2, 0, 64, None) == -2            # N = 0
     assert f(P16, P16, P16, P16, P16, 2, 8, 65536, None) == -5         # K > NVE_MAX_K
-    assert f(P16, P16, P16 + 2, P16, P16, 2, 8, 64, None) == -3        # nibbles not 16B aligned
-    assert f(P16 + 4, P16, P16, P16, P16, 2, 8, 64, None) == -3        # xq not 16B aligned
+    # the reference's contract: nibbles 2-byte, xq 4-byte aligned (the main kernels need
+    # 16; weaker alignment down to the contract is served, below it refused)
+    assert f(P16, P16, P16 + 1, P16, P16, 2, 8, 64, None) == -3        # nibbles odd
+    assert f(P16 + 2, P16, P16, P16, P16, 2, 8, 64, None) == -3        # xq not 4-byte aligned
     assert f(P16, P16, P16, P16, P16, 7, 8, 64, None) == -4            # out dtype
     assert L.nve_hip_last_status() == -4
 
@@ -68,7 +70,8 @@ def test_w4a16_argument_errors(L):
     f = L.nve_hip_matvec_w4a16
     assert f(None, 0, P16, P16, None, P16, 0, 8, 64, None) == -1
     assert f(P16, 2, P16, P16, None, P16, 0, 8, 64, None) == -4        # f32 x not accepted
-    assert f(P16, 0, P16, P16, P16 + 4, P16, 0, 8, 64, None) == -3     # awq misaligned
+    assert f(P16, 0, P16, P16, P16 + 2, P16, 0, 8, 64, None) == -3     # awq not 4-byte aligned
+    assert f(P16 + 1, 0, P16, P16, None, P16, 0, 8, 64, None) == -3    # fp16 x odd
     assert f(P16, 0, P16, P16, None, P16, 0, -1, 64, None) == -2
 
 
@@ -77,7 +80,8 @@ def test_batched_and_prep_argument_errors(L):
     assert L.nve_hip_matvec_w4a8_batched(17, P16, P16, 0, P16, P16, P16, 2, 8, 64, None) == -2
     assert L.nve_hip_matvec_w4a8_batched(4, P16, P16, 5, P16, P16, P16, 2, 8, 64, None) == -4
     assert L.nve_hip_quantize_q8(P16, 0, 1, 40, P16, P16, None) == -2
-    assert L.nve_hip_quantize_q8(P16 + 2, 0, 1, 64, P16, P16, None) == -3
+    assert L.nve_hip_quantize_q8(P16 + 1, 0, 1, 64, P16, P16, None) == -3   # fp16 x odd
+    assert L.nve_hip_quantize_q8(P16 + 2, 2, 1, 64, P16, P16, None) == -3   # f32 x not 4-byte aligned
     assert L.nve_hip_quantize_q8_rows(P16, 9, 1, 64, P16, P16, None) == -4
     assert L.nve_hip_q4_quantize(P16, 2, 4, 33, P16, P16, None) == -2
     assert L.nve_hip_q4_repack(P16, 4, 64, P16 + 8, P16, None) == -3

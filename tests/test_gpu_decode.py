@@ -42,9 +42,11 @@ def _model(torch, heads, kv, d, *, layers=3, hidden=256, ffn=512, vocab=512, max
                        seed=seed)
 
 
-def _run_teacher_forced(torch, m, steps, token0=5):
+def _run_teacher_forced(torch, m, steps, token0=5, checked=None, record=None):
     """Layer by layer: the oracle's layer i starts from the GPU's hidden state before
-    layer i, so every layer and the head are checked on their own."""
+    layer i, so every layer and the head are checked on their own.  checked: the layers
+    to compare (None = all; the others only run).  record: a list that receives each
+    step's (token, logits)."""
     from oracle import decode_ref as dr
     hm = dr.HostModel(m)
     m.start(token0)
@@ -54,6 +56,9 @@ def _run_teacher_forced(torch, m, steps, token0=5):
         print(f"decode step {i} pos {pos}", flush=True)
         m._advance(1)
         for li in range(m.shape.layers):
+            if checked is not None and li not in checked:
+                m.layer(li)
+                continue
             torch.cuda.synchronize()
             h_in = m.hidden.cpu().numpy().copy()
             m.layer(li)
@@ -82,6 +87,8 @@ def _run_teacher_forced(torch, m, steps, token0=5):
         top = np.sort(o_logits)[-2:]
         if top[1] - top[0] > 4 * TOL_LAYER * np.linalg.norm(o_logits) / np.sqrt(o_logits.size):
             assert g_tok == o_tok, (i, g_tok, o_tok)
+        if record is not None:
+            record.append((g_tok, g_logits.copy()))
         # the head embedded the GPU's token and advanced the position
         assert np.array_equal(m.hidden.cpu().numpy(), hm.embed[g_tok])
         assert int(m.pos.item()) == pos + 1
@@ -238,3 +245,26 @@ def test_decode_from_checkpoint(torch_dev, tmp_path, tied):
     assert torch.equal(m.lm_head[0], nib) and torch.equal(m.lm_head[1], sc)
     _run_teacher_forced(torch, m, steps=3)
 
+
+
+def test_decode_bench_model_sampled_layers(torch_dev):
+    """The bench's own decode model (Llama-3.2-3B shapes, 28 layers with the seeded
+    8 W4A16 / 20 W4A8 mask, W4A8 lm_head, 512 cached keys in a 1024-slot cache, four-way
+    key-split attention): layers 0, 13 and 27 and the head teacher-forced against the
+    oracle for two tokens, then the captured HIP graph replays the same two tokens bit
+    for bit."""
+    torch = torch_dev
+    from nve_amd.decode import LLAMA_3_2_3B, DecodeModel
+    m = DecodeModel(LLAMA_3_2_3B, max_seq=1024, prefill=512)
+    assert sum(1 for u in m.use_w4a8 if not u) == 8
+    checked = {0, 13, 27}
+    print("bench model: layer precisions (1 = W4A8)", [m.use_w4a8[i] for i in sorted(checked)], flush=True)
+    rec = []
+    _run_teacher_forced(torch, m, steps=2, token0=1, checked=checked, record=rec)
+    m.start(1)
+    m.capture()
+    for r in range(2):
+        m.generate(1)
+        torch.cuda.synchronize()
+        assert int(m.token.item()) == rec[r][0], r
+        assert np.array_equal(m.logits.cpu().numpy(), rec[r][1]), r

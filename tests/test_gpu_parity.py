@@ -392,9 +392,10 @@ def test_dequant_w4a16_drop_in(orc, torch_dev, hk):
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("per_token", [False, True])
-def test_w4a8_batched_parity(orc, torch_dev, hk, m, per_token):
+@pytest.mark.parametrize("n,k", [(300, 4096), (14336, 4096)])
+def test_w4a8_batched_parity(orc, torch_dev, hk, m, per_token, n, k):
+    """configs[3] at the Llama-3.1-8B gate shape (and a small ragged one)."""
     torch = torch_dev
-    n, k = 300, 4096
     _, _, nib, ws = _problem(orc, n, k, seed=m)
     x = to_bf16(activations(k, seed=200 + m, m=m))
     xq, xs = hk.quantize_q8_rows(up(torch, x).to(torch.bfloat16), per_token=per_token)
@@ -467,7 +468,7 @@ def test_dispatch_project(orc, torch_dev, hk, monkeypatch):
 
 @pytest.mark.parametrize("m", [2, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("n,k", [(16, 32), (17, 96), (300, 160), (1000, 2048), (8200, 4096), (70, 14336),
-                                 (4096, 14336)])
+                                 (4096, 14336), (14336, 4096)])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
     """M >= 2 runs on the int8 MFMA kernel: ragged N, K with a partial last block quad

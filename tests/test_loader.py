@@ -60,7 +60,7 @@ def test_q4_block_file_errors(tmp_path):
 
 
 def test_shape_from_hf_config():
-    """config.json fields -> ModelShape (the fields src/config.rs reads)."""
+    """config.json fields -> ModelShape (the fields src/arch.rs:200-262 reads)."""
     from nve_amd.decode import ModelShape, shape_from_hf_config
     cfg = {"hidden_size": 3072, "num_hidden_layers": 28, "num_attention_heads": 24, "num_key_value_heads": 8,
            "intermediate_size": 8192, "vocab_size": 128256, "rms_norm_eps": 1e-5, "rope_theta": 500000.0,
@@ -77,6 +77,8 @@ def test_shape_from_hf_config():
     assert isinstance(s, ModelShape)
     with pytest.raises(ValueError):
         shape_from_hf_config({**cfg, "rope_scaling": {"rope_type": "yarn", "factor": 4.0}})
+    # rope_type "default" is no scaling
+    assert shape_from_hf_config({**cfg, "rope_scaling": {"rope_type": "default"}}).rope_scaling is None
 
 
 def test_checkpoint_weights_rejects_mismatch():
@@ -95,3 +97,13 @@ def test_checkpoint_weights_rejects_mismatch():
     w[p + "self_attn.q_proj.weight"] = torch.ones(64, 64)  # stored dense: not quantized on load
     with pytest.raises(ValueError):
         checkpoint_weights(w, s, device="cpu")
+
+
+def test_checkpoint_weights_untied_needs_lm_head():
+    """tie_word_embeddings = false and no lm_head.weight: a KeyError, not a silent tie."""
+    from nve_amd.decode import ModelShape, checkpoint_weights
+    s = ModelShape(hidden=64, layers=0, heads=2, kv_heads=1, head_dim=32, ffn=128, vocab=64)
+    import torch
+    w = {"model.embed_tokens.weight": torch.ones(64, 64), "model.norm.weight": torch.ones(64)}
+    with pytest.raises(KeyError, match="lm_head"):
+        checkpoint_weights(w, s, device="cpu", tie_word_embeddings=False)
