@@ -225,18 +225,23 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * rounds it (to x's dtype: F16 as the reference, or BF16) and the products accumulate
  * in fp32 on MFMA (M <= 16: a weight-streaming kernel; larger M: LDS-tiled).  x [M, K]
  * row-major F16/BF16 (16-byte aligned); awq [K] or NULL; out [M, N] row-major F16,
- * BF16 or F32.  K % 64 == 0. */
+ * BF16 or F32.  K % 64 == 0.  With F32 output and a tile grid too small to fill the
+ * GPU, K is split over workgroups whose fp32 partials are added atomically: the last
+ * bits of such an output may differ from call to call (nve_hip_gemm_w4a16_ws with its
+ * workspace is bit-reproducible). */
 int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,
                        const float *awq, void *out, int out_dtype, int N, int K, void *stream);
 
 /* The same product with the reference's own two-step method where it is faster
- * (GpuWeight::matmul_x, src/gpu_layer.rs:219-237): for M >= 512, with a workspace of at
- * least nve_hip_gemm_w4a16_workspace_bytes(M, N, K) bytes (256-byte aligned) and out
- * F32 or x's dtype, the weights are dequantized into the workspace (nve_hip_dequant_w4,
- * bit-identical to the reference dequant) and multiplied by hipBLASLt (fp32
- * accumulation); otherwise it runs nve_hip_gemm_w4a16.  The first call per device and
+ * (GpuWeight::matmul_x, src/gpu_layer.rs:219-237), and bit-reproducible everywhere.
+ * The workspace (nve_hip_gemm_w4a16_workspace_bytes(M, N, K) bytes, 256-byte aligned)
+ * holds: for M >= 512, with out F32 or x's dtype, the weights dequantized by
+ * nve_hip_dequant_w4 (bit-identical to the reference dequant), which hipBLASLt then
+ * multiplies with fp32 accumulation; otherwise the fp32 partials of the fused kernel's
+ * K split, added in a fixed order (0 bytes when the shape does not split).  With a NULL
+ * or smaller workspace it runs nve_hip_gemm_w4a16.  The first call per device and
  * shape creates the hipBLASLt handle and selects the algorithm; made under graph
- * capture, such a call runs nve_hip_gemm_w4a16 instead, so make it once before
+ * capture, such a call runs the fused kernel instead, so make it once before
  * capturing.  No counterpart in the reference's FFI (it makes two calls). */
 size_t nve_hip_gemm_w4a16_workspace_bytes(int M, int N, int K);
 int nve_hip_gemm_w4a16_ws(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,

@@ -25,6 +25,10 @@ hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib,
                              void* out, int out_dt, int N, int K, hipStream_t s);
 hipError_t launch_dequant_w4(const uint8_t* nib, const float* scales, const float* awq, void* out, int out_dt,
                              int N, int K, hipStream_t stream);
+hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
+                                   const float* awq, void* out, int out_dt, int N, int K, float* parts,
+                                   size_t parts_bytes, hipStream_t s);
+size_t gemm_split_parts_bytes(int M, int N, int K);
 
 namespace {
 
@@ -132,9 +136,13 @@ AlgoChoice select_algo(hipblasLtHandle_t h, const Descs& ds, const void* x, void
 
 }  // namespace
 
+// Below kGemmBlasMinM: the fp32 partials of the fused kernel's K split (0 when that
+// shape does not split); from it on: the dequantized weights + the hipBLASLt workspace.
 size_t gemm_w4a16_ws_bytes(int M, int N, int K) {
-  if (M < kGemmBlasMinM) return 0;
-  return round256((size_t)N * K * 2) + kBlasWorkspace;
+  if (M < kGemmBlasMinM) return round256(gemm_split_parts_bytes(M, N, K));
+  const size_t blas = round256((size_t)N * K * 2) + kBlasWorkspace;
+  const size_t parts = round256(gemm_split_parts_bytes(M, N, K));
+  return blas > parts ? blas : parts;
 }
 
 // Dequant + hipBLASLt when M >= kGemmBlasMinM, the workspace is large enough and the
@@ -145,9 +153,13 @@ size_t gemm_w4a16_ws_bytes(int M, int N, int K) {
 hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
                                 const float* awq, void* out, int out_dt, int N, int K, void* ws, size_t ws_bytes,
                                 hipStream_t s) {
-  const size_t need = gemm_w4a16_ws_bytes(M, N, K);
-  if (need == 0 || ws == nullptr || ws_bytes < need || (out_dt != NVE_DT_F32 && out_dt != x_dt))
-    return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
+  // the fused kernel, with its K-split partials (if any) in the workspace: added in a
+  // fixed order, so the result does not vary between calls
+  auto fused = [&]() {
+    return launch_gemm_w4a16_parts(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, (float*)ws, ws ? ws_bytes : 0, s);
+  };
+  const size_t need = M >= kGemmBlasMinM ? round256((size_t)N * K * 2) + kBlasWorkspace : 0;
+  if (need == 0 || ws == nullptr || ws_bytes < need || (out_dt != NVE_DT_F32 && out_dt != x_dt)) return fused();
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -169,8 +181,7 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
     if (known) choice = ai->second;
     // Handle creation and the first call's timing (event synchronisation) cannot run
     // under graph capture: an unseen device or shape is served by the fused kernel.
-    if (capturing && (hi == g_handles.end() || !known))
-      return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
+    if (capturing && (hi == g_handles.end() || !known)) return fused();
     if (hi == g_handles.end()) {
       if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return hipErrorNotSupported;
       g_handles[dev] = h;
@@ -186,7 +197,7 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
     std::lock_guard<std::mutex> lk(g_mu);
     choice = g_algo.emplace(key, choice).first->second;
   }
-  if (!choice.ok) return launch_gemm_w4a16(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, s);
+  if (!choice.ok) return fused();
   const hipblasLtMatmulAlgo_t algo = choice.algo;
   void* wdq = ws;
   void* blas_ws = (char*)ws + round256((size_t)N * K * 2);

@@ -133,10 +133,14 @@ __device__ __forceinline__ void gemm_mfma(const uint16_t* sX, const uint16_t* sW
   }
 }
 
-// SPLIT: the K range is divided over gridDim.z workgroups per output tile, which add
-// their fp32 partial sums into a zeroed fp32 output (launches whose tile grid alone
-// would leave most CUs idle: small M).
-template <bool BF16, bool AWQ, int OUT_DT, bool SPLIT>
+// SPLIT: the K range is divided over gridDim.z workgroups per output tile (launches
+// whose tile grid alone would leave most CUs idle: small M).  SPLIT_ATOMIC: the
+// workgroups add their fp32 partial sums into a zeroed fp32 output (the order of the
+// additions varies from run to run); SPLIT_PARTS: workgroup z stores its partial
+// tile to out + z * M * N and split_reduce_kernel adds the partials in the order
+// z = 0, 1, ... (bit-reproducible).
+enum { SPLIT_NONE = 0, SPLIT_ATOMIC = 1, SPLIT_PARTS = 2 };
+template <bool BF16, bool AWQ, int OUT_DT, int SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_w4a16_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ nib, const float* __restrict__ scales,
     const float* __restrict__ awq, void* __restrict__ out, int M, int N, int K, int k_split) {
@@ -196,8 +200,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < M && n < N) {
-          if (SPLIT)
+          if (SPLIT == SPLIT_ATOMIC)
             atomicAdd((float*)out + (size_t)m * N + n, acc[i][j][r]);
+          else if (SPLIT == SPLIT_PARTS)
+            ((float*)out)[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = acc[i][j][r];
           else
             store_out<OUT_DT>(out, (size_t)m * N + n, acc[i][j][r]);
         }
@@ -375,6 +381,16 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
   }
 }
 
+// out[i] = sum over z = 0 .. split-1 of part[z * n + i], in that order.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                           size_t n, int split) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float y = part[i];
+  for (int z = 1; z < split; ++z) y += part[(size_t)z * n + i];
+  out[i] = y;
+}
+
 __global__ __launch_bounds__(256) void zero_f32_kernel(float4* __restrict__ p, size_t n4) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n4) p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -390,18 +406,42 @@ namespace nve_host {
 constexpr int kGemmSmallM = 16;
 constexpr int kSmallKS = 16;
 
-template <bool BF16, bool AWQ>
-static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
-                                void* out, int out_dt, int N, int K, hipStream_t s) {
+// K splits of the tiled kernel: split while the tile grid covers fewer than 512
+// workgroups (two per CU), keeping at least 4 K iterations per split; fp32 output only.
+static int gemm_split(int M, int N, int K, int out_dt) {
   const int tn = (N + nve::GM_BN - 1) / nve::GM_BN, tm = (M + nve::GM_BM - 1) / nve::GM_BM;
-  // split K while the tile grid covers fewer than 512 workgroups (two per CU), keeping
-  // at least 4 K iterations per split; fp32 output only (partials are added atomically)
   int split = 1;
   const int kit = K / nve::GM_BK;
-  if (out_dt == NVE_DT_F32)
+  if (out_dt == NVE_DT_F32 && M > kGemmSmallM)
     while (tn * tm * split < 512 && kit / (2 * split) >= 4) split *= 2;
-  if (split > 1) {
-    const size_t n = (size_t)M * N;  // M * N * 4 bytes; zeroed with float4 stores when possible
+  return split;
+}
+
+// Bytes of fp32 partials the bit-reproducible split needs (0: no split).
+size_t gemm_split_parts_bytes(int M, int N, int K) {
+  const int split = gemm_split(M, N, K, NVE_DT_F32);
+  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+}
+
+// parts: NULL -> a split launch adds its partials atomically into a zeroed output;
+// else (parts_bytes >= gemm_split_parts_bytes) the partials go to `parts` and are added
+// in a fixed order.
+template <bool BF16, bool AWQ>
+static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                                void* out, int out_dt, int N, int K, float* parts, size_t parts_bytes,
+                                hipStream_t s) {
+  const int tn = (N + nve::GM_BN - 1) / nve::GM_BN, tm = (M + nve::GM_BM - 1) / nve::GM_BM;
+  int split = gemm_split(M, N, K, out_dt);
+  const int kit = K / nve::GM_BK;
+  const size_t n = (size_t)M * N;
+  bool use_parts = false;
+  if (split > 1 && parts) {
+    if (parts_bytes >= (size_t)split * n * sizeof(float))
+      use_parts = true;
+    else
+      split = 1;  // a workspace too small for the partials: no split (still reproducible)
+  } else if (split > 1) {
+    // M * N * 4 bytes zeroed with float4 stores when possible
     if (n % 4 == 0 && ((uintptr_t)out & 15) == 0) {
       hipLaunchKernelGGL(nve::zero_f32_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, (float4*)out, n / 4);
     } else {
@@ -410,16 +450,20 @@ static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const 
   }
   const int k_split = ((kit + split - 1) / split) * nve::GM_BK;
   const dim3 grid(tn, tm, split);
-#define NVE_GEMM(OD, SP)                                                                                       \
+#define NVE_GEMM(OD, SP, O)                                                                                    \
   hipLaunchKernelGGL((nve::gemm_w4a16_kernel<BF16, AWQ, OD, SP>), grid, dim3(256), 0, s, (const uint16_t*)x, nib, \
-                     sc, awq, out, M, N, K, k_split)
-  if (split > 1) {
-    NVE_GEMM(NVE_DT_F32, true);
+                     sc, awq, O, M, N, K, k_split)
+  if (split > 1 && use_parts) {
+    NVE_GEMM(NVE_DT_F32, nve::SPLIT_PARTS, (void*)parts);
+    hipLaunchKernelGGL(nve::split_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, parts,
+                       (float*)out, n, split);
+  } else if (split > 1) {
+    NVE_GEMM(NVE_DT_F32, nve::SPLIT_ATOMIC, out);
   } else {
     switch (out_dt) {
-      case NVE_DT_F16: NVE_GEMM(NVE_DT_F16, false); break;
-      case NVE_DT_BF16: NVE_GEMM(NVE_DT_BF16, false); break;
-      default: NVE_GEMM(NVE_DT_F32, false); break;
+      case NVE_DT_F16: NVE_GEMM(NVE_DT_F16, nve::SPLIT_NONE, out); break;
+      case NVE_DT_BF16: NVE_GEMM(NVE_DT_BF16, nve::SPLIT_NONE, out); break;
+      default: NVE_GEMM(NVE_DT_F32, nve::SPLIT_NONE, out); break;
     }
   }
 #undef NVE_GEMM
@@ -451,8 +495,9 @@ static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const f
   }
 }
 
-hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, const float* awq,
-                             void* out, int out_dt, int N, int K, hipStream_t s) {
+hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
+                                   const float* awq, void* out, int out_dt, int N, int K, float* parts,
+                                   size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
   if (M <= kGemmSmallM) {
     if (awq) return bf ? launch_small<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, s)
@@ -460,10 +505,15 @@ hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib,
     return bf ? launch_small<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, s)
               : launch_small<false, false>(x, M, nib, sc, awq, out, out_dt, N, K, s);
   }
-  if (awq) return bf ? launch_gemm_t<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, s)
-                     : launch_gemm_t<false, true>(x, M, nib, sc, awq, out, out_dt, N, K, s);
-  return bf ? launch_gemm_t<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, s)
-            : launch_gemm_t<false, false>(x, M, nib, sc, awq, out, out_dt, N, K, s);
+#define NVE_GT(B, A) launch_gemm_t<B, A>(x, M, nib, sc, awq, out, out_dt, N, K, parts, parts_bytes, s)
+  if (awq) return bf ? NVE_GT(true, true) : NVE_GT(false, true);
+  return bf ? NVE_GT(true, false) : NVE_GT(false, false);
+#undef NVE_GT
+}
+
+hipError_t launch_gemm_w4a16(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, const float* awq,
+                             void* out, int out_dt, int N, int K, hipStream_t s) {
+  return launch_gemm_w4a16_parts(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, nullptr, 0, s);
 }
 
 }  // namespace nve_host

@@ -163,7 +163,10 @@ def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
     (compared at fp16 output: fp32 output at small M splits K with atomic adds, whose
     order is not fixed)."""
     torch = torch_dev
-    assert hk.gemm_w4a16_workspace_bytes(511, 256, 1024) == 0 and hk.gemm_w4a16_workspace_bytes(512, 256, 1024) > 0
+    # below M = 512 the workspace holds only K-split partials (none for M <= 16)
+    assert hk.gemm_w4a16_workspace_bytes(16, 256, 1024) == 0
+    assert hk.gemm_w4a16_workspace_bytes(511, 256, 1024) == 4 * 511 * 256 * 4
+    assert hk.gemm_w4a16_workspace_bytes(512, 256, 1024) > (256 * 1024 * 2)
     n, k = 256, 1024
     data = orc.q4_from_f32(weights(n, k, seed=5, std=0.05))
     nib, sc = (torch.from_numpy(a).cuda() for a in orc.extract_for_gpu(data, n, k))
@@ -205,3 +208,39 @@ def test_gemm_w4a16_ws_graph_capture(orc, torch_dev, hk):
                 assert torch.equal(out, eager)
             else:
                 assert torch.equal(out, eager_fused)
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 512, 4096), (40, 1000, 2048), (200, 256, 8192)])
+def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
+    """With a workspace, a K-split fp32 product stores its partials there and adds them
+    in a fixed order: every call -- eager or replayed from a HIP graph -- gives the same
+    bits, within the W4A16 bar of the oracle and within fp32 rounding of the atomic
+    split of nve_hip_gemm_w4a16."""
+    torch = torch_dev
+    wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
+    assert wsb > 0
+    data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.05))
+    nib_h, sc_h = orc.extract_for_gpu(data, n, k)
+    nib, sc = torch.from_numpy(nib_h).cuda(), torch.from_numpy(sc_h).cuda()
+    xh = np.random.default_rng(m).standard_normal((m, k)).astype(np.float16)
+    x = torch.from_numpy(xh).cuda()
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    a = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
+    b = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
+    atomic = hk.gemm_w4a16(x, nib, sc, n, k)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out.copy_(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws))
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, a)
+    assert torch.equal(a, b)
+    assert torch.allclose(a, atomic, rtol=1e-5, atol=1e-5 * float(a.abs().max()))
+    wref = _round(orc.q4_to_f32(data, n, k, None), "f16").astype(np.float64)
+    ref = xh.astype(np.float64) @ wref.T
+    assert rel_err_floor(a.cpu().numpy(), ref) <= 2e-3
