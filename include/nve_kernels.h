@@ -335,6 +335,16 @@ size_t nve_hip_decode_workspace_bytes(const nve_decode_config *cfg);
  * nve_use_w4a8). */
 int nve_hip_layer_forward_decode(const nve_decode_config *cfg, const nve_layer_weights *w,
                                  const nve_decode_io *io, int use_w4a8, void *stream);
+/* The same layer without a caller workspace.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  io->workspace is not read (may be
+ * NULL); the scratch is a 1 MiB array inside the library, one per GPU, held until the
+ * process ends and looked up once per device.  Nothing is allocated on any call.
+ * Layers whose workspace (nve_hip_decode_workspace_bytes of cfg with vocab = 0) exceeds
+ * 1 MiB return NVE_ERR_TOO_LARGE.  Calls that overlap on one GPU (concurrent streams)
+ * share the array and race; every call writes the scratch it reads. */
+int nve_hip_layer_forward_decode_noalloc(const nve_decode_config *cfg, const nve_layer_weights *w,
+                                         const nve_decode_io *io, int use_w4a8, void *stream);
 /* Final RMSNorm, lm_head GEMV (fp32 logits), greedy argmax, embedding of the chosen
  * token into hidden, *pos += 1. */
 int nve_hip_decode_head(const nve_decode_config *cfg, const nve_decode_head *head, int use_w4a8,

@@ -57,6 +57,7 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_set_gemv_policy": (_i, [_i, _i, _i]),
     "nve_hip_decode_workspace_bytes": (C.c_size_t, [_p]),
     "nve_hip_layer_forward_decode": (_i, [_p, _p, _p, _i, _p]),
+    "nve_hip_layer_forward_decode_noalloc": (_i, [_p, _p, _p, _i, _p]),
     "nve_hip_decode_head": (_i, [_p, _p, _i, _p]),
     "nve_hip_embed": (_i, [_p, _p, _p, _i, _p]),
     "nve_hip_last_status": (_i, []),

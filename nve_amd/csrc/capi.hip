@@ -417,24 +417,39 @@ static int check_w4(const nve_w4_weight& w, int n, int k) {
   return NVE_OK;
 }
 
-int nve_hip_layer_forward_decode(const nve_decode_config* cfg, const nve_layer_weights* w, const nve_decode_io* io,
-                                 int use_w4a8, void* stream) {
-  if (!cfg || !w || !io) return set_status(NVE_ERR_NULL);
+// Arguments of the decode layer; need_ws: the caller passes the workspace.
+static int check_layer_args(const nve_decode_config* cfg, const nve_layer_weights* w, const nve_decode_io* io,
+                            bool need_ws) {
+  if (!cfg || !w || !io) return NVE_ERR_NULL;
   int st = check_decode(*cfg);
-  if (st != NVE_OK) return set_status(st);
+  if (st != NVE_OK) return st;
   const int H = cfg->hidden, F = cfg->ffn, QD = cfg->num_heads * cfg->head_dim,
             KD = cfg->num_kv_heads * cfg->head_dim;
   const nve_w4_weight* mats[7] = {&w->q, &w->k, &w->v, &w->o, &w->gate, &w->up, &w->down};
   const int ns[7] = {QD, KD, KD, H, F, F, H}, ks[7] = {H, H, H, QD, H, H, F};
   for (int i = 0; i < 7; ++i)
-    if ((st = check_w4(*mats[i], ns[i], ks[i])) != NVE_OK) return set_status(st);
+    if ((st = check_w4(*mats[i], ns[i], ks[i])) != NVE_OK) return st;
   if (!w->input_norm || !w->post_attn_norm || !io->hidden || !io->k_cache || !io->v_cache || !io->pos ||
-      !io->rope_cos || !io->rope_sin || !io->workspace)
-    return set_status(NVE_ERR_NULL);
-  if (!aligned(io->workspace, 256) || !aligned(io->hidden, 16) || !aligned(io->k_cache, 16) ||
+      !io->rope_cos || !io->rope_sin || (need_ws && !io->workspace))
+    return NVE_ERR_NULL;
+  if ((need_ws && !aligned(io->workspace, 256)) || !aligned(io->hidden, 16) || !aligned(io->k_cache, 16) ||
       !aligned(io->v_cache, 16))
-    return set_status(NVE_ERR_ALIGN);
+    return NVE_ERR_ALIGN;
+  return NVE_OK;
+}
+
+int nve_hip_layer_forward_decode(const nve_decode_config* cfg, const nve_layer_weights* w, const nve_decode_io* io,
+                                 int use_w4a8, void* stream) {
+  const int st = check_layer_args(cfg, w, io, true);
+  if (st != NVE_OK) return set_status(st);
   return set_status(layer_forward_decode(*cfg, *w, *io, use_w4a8 != 0, (hipStream_t)stream));
+}
+
+int nve_hip_layer_forward_decode_noalloc(const nve_decode_config* cfg, const nve_layer_weights* w,
+                                         const nve_decode_io* io, int use_w4a8, void* stream) {
+  const int st = check_layer_args(cfg, w, io, false);
+  if (st != NVE_OK) return set_status(st);
+  return set_status(layer_forward_decode_noalloc(*cfg, *w, *io, use_w4a8 != 0, (hipStream_t)stream));
 }
 
 int nve_hip_decode_head(const nve_decode_config* cfg, const nve_decode_head* hd, int use_w4a8, void* stream) {

@@ -706,3 +706,56 @@ hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, 
 int check_decode(const nve_decode_config& c) { return check_cfg(c); }
 
 }  // namespace nve_host
+
+// ---------------------------------------------------------------------------
+// The decode layer without a caller workspace (nve_hip_layer_forward_decode_noalloc):
+// its scratch is a file-scope device array, one copy per GPU, whose address is looked
+// up once per device with hipGetSymbolAddress.  No allocation happens on any call, so
+// the entry point can run where hipMalloc cannot (under graph capture, in serving
+// loops).  Calls that overlap on one GPU (concurrent streams) share the array and race.
+// ---------------------------------------------------------------------------
+namespace nve {
+constexpr size_t kDecodeScratchBytes = 1u << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+}  // namespace nve
+
+#include <mutex>
+
+namespace nve_host {
+
+// Device address of this GPU's scratch array (the host-side symbol is only a handle).
+static hipError_t decode_scratch_ptr(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(nve::scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return hipSuccess;
+}
+
+int layer_forward_decode_noalloc(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
+                                 bool w4a8, hipStream_t s) {
+  // the layer reads no logits: lay the workspace out without them
+  nve_decode_config cl = c;
+  cl.vocab = 0;
+  if (decode_workspace_bytes(cl) > nve::kDecodeScratchBytes) return NVE_ERR_TOO_LARGE;
+  void* p = nullptr;
+  const hipError_t e = decode_scratch_ptr(&p);
+  if (e != hipSuccess) return (int)e;
+  nve_decode_io io2 = io;
+  io2.workspace = p;
+  return layer_forward_decode(cl, w, io2, w4a8, s);
+}
+
+}  // namespace nve_host

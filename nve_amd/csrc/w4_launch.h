@@ -184,6 +184,8 @@ int check_decode(const nve_decode_config& c);
 int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                          bool w4a8, hipStream_t s);
 int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8, hipStream_t s);
+int layer_forward_decode_noalloc(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
+                                 bool w4a8, hipStream_t s);
 // Fused-producer GEMVs (act_producer.h); swiglu pairs gate (slot 0) with up (nib[1],
 // sc[1]) and writes silu(gate) * up.
 }  // namespace nve_host
