@@ -654,6 +654,22 @@ def batched_probe(torch, L, hk):
     print(json.dumps({"probe": "batched", "order": order}), flush=True)
 
 
+def suite_probe(torch, L, hk):
+    """The per-shape tables of the bench (8B suite, both precisions, grouped launches;
+    batched W4A8 sweep) on their own, for a rocprofv3 kernel trace: each (shape,
+    precision) runs as graphs of back-to-back launches separated by host
+    synchronisations, in the order printed at the end."""
+    weights = make_inputs(torch, hk, 8, 4)
+    acts = {}
+    for nm, k, sd in (("h", 4096, 1), ("mid", 14336, 4)):
+        x = make_activation(torch, k, sd)
+        acts[nm + "16"] = x.to(torch.float16)
+        acts[nm + "b"] = x.to(torch.bfloat16)
+    table = kernel_table(torch, L, weights, acts)
+    sweep = batched_sweep(torch, L, weights)
+    print(json.dumps({"probe": "suite", "order": list(table) + list(sweep)}), flush=True)
+
+
 def traffic_probe(torch, L, hk):
     """Short run for rocprofv3 --pmc (FETCH_SIZE / WRITE_SIZE): a plain device copy of
     256 MiB (calibration: 256 MiB read + 256 MiB written), then the step's two lm_head
@@ -713,6 +729,9 @@ def main():
                     help="short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (no bench line)")
     ap.add_argument("--batched-probe", action="store_true",
                     help="eager batched W4A8 launches for rocprofv3 --pmc MFMA counters (no bench line)")
+    ap.add_argument("--suite-probe", action="store_true",
+                    help="only the per-shape 8B table and the batched sweep, for rocprofv3 --kernel-trace "
+                         "per-shape kernel durations (no bench line)")
     ap.add_argument("--decode-traffic-probe", action="store_true",
                     help="6 eager (not graph-replayed) 3B decode steps for rocprofv3 --pmc (no bench line)")
     args = ap.parse_args()
@@ -737,6 +756,9 @@ def main():
         return
     if args.batched_probe:
         batched_probe(torch, L, hk)
+        return
+    if args.suite_probe:
+        suite_probe(torch, L, hk)
         return
     if args.decode_only:
         print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True,

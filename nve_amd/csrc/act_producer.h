@@ -17,8 +17,8 @@
 //             epilogue of the gate/up GEMV); b unused.
 //   SRC_F16 / SRC_BF16: x_k = a_k of a 16-bit vector (the W4A8 GEMV that quantizes its
 //             own activations: nve_quantize_f16_q8 + nve_matvec_w4a8 in one launch).
-//   SRC_ATTN2 / 4 / 8: the decode attention output, merged from the partials of 2, 4
-//             or 8 key splits: a = records [split][head] of (m, l, -, -, acc[D]) with
+//   SRC_ATTN1 / 2 / 4 / 8: the decode attention output, merged from the partials of 1,
+//             2, 4 or 8 key splits: a = records [split][head] of (m, l, -, -, acc[D]) with
 //             m the running max of the scores in log2 units (q . k * log2(e) / sqrt(D)),
 //             l the sum of 2^(s - m), acc the unnormalised value sum;
 //             x = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s (M = max_s m_s);
@@ -29,10 +29,13 @@
 
 namespace nve {
 
-enum { SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2, SRC_F16 = 3, SRC_BF16 = 4, SRC_ATTN2 = 5, SRC_ATTN4 = 6, SRC_ATTN8 = 7 };
+enum {
+  SRC_PLAIN = 0, SRC_NORM = 1, SRC_F32 = 2, SRC_F16 = 3, SRC_BF16 = 4, SRC_ATTN2 = 5, SRC_ATTN4 = 6, SRC_ATTN8 = 7,
+  SRC_ATTN1 = 8
+};
 
 __host__ __device__ constexpr int attn_splits_of(int src) {
-  return src == SRC_ATTN2 ? 2 : (src == SRC_ATTN4 ? 4 : (src == SRC_ATTN8 ? 8 : 0));
+  return src == SRC_ATTN2 ? 2 : (src == SRC_ATTN4 ? 4 : (src == SRC_ATTN8 ? 8 : (src == SRC_ATTN1 ? 1 : 0)));
 }
 
 struct ProdArgs {
