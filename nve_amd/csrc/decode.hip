@@ -111,7 +111,9 @@ __device__ __forceinline__ void attn_issue(AttnTile<D>& b, const uint16_t* __res
   }
 }
 
-template <int D>
+// NEWROW: the row at pos comes from the workgroup's own copy in LDS (s_knew / s_vnew)
+// rather than the cache (which this launch writes).
+template <int D, bool NEWROW = true>
 __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int len, int pos, int wave, int krow,
                                              int col, const float (&qv)[8], const uint16_t* s_knew,
                                              const uint16_t* s_vnew, float& m_run, float& l_run, float (&acc)[8]) {
@@ -121,7 +123,7 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
 #pragma unroll
   for (int i = 0; i < T::P; ++i) {
     const int key = t * T::KT + (i * T::NW + wave) * T::KPW + krow;
-    const uint4 kr = key == pos ? *(const uint4*)(s_knew + col * 8) : b.k[i];
+    const uint4 kr = (NEWROW && key == pos) ? *(const uint4*)(s_knew + col * 8) : b.k[i];
     const uint32_t w[4] = {kr.x, kr.y, kr.z, kr.w};
     float d = 0.0f;
 #pragma unroll
@@ -148,7 +150,8 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
     const float p = exp2f(s[i] - m_run);  // masked keys: exp2(-inf) = 0
     l_run += p;
     // rows past the length may hold anything (even NaN): they must not reach acc
-    const uint4 vr = key == pos ? *(const uint4*)(s_vnew + col * 8) : (key < len ? b.v[i] : make_uint4(0, 0, 0, 0));
+    const uint4 vr = (NEWROW && key == pos) ? *(const uint4*)(s_vnew + col * 8)
+                                             : (key < len ? b.v[i] : make_uint4(0, 0, 0, 0));
     const uint32_t w[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -158,104 +161,16 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
   }
 }
 
-// SPLIT > 1 (OUT 3): workgroup (head, sp) takes the tiles t = sp, sp + SPLIT, ... and
-// writes its partial state (m, l, 0, 0, acc[D]) -- m in log2 units, acc not yet
-// divided by l -- to out_part[sp][head]; the consumer merges the SPLIT partials
-// (act_producer.h, SRC_ATTN2 / 4 / 8).  A split with no tile writes m = -inf, l = 0, acc = 0.
-template <int D, int OUT, int SPLIT = 1>
-__global__ __launch_bounds__(1024) void attn_decode_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
-    int max_seq, float qscale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
-    float* __restrict__ out_s, float* __restrict__ out_part, int xcd_map) {
-  static_assert((OUT == 3) == (SPLIT > 1), "split partials go to out_part");
+// Merge of the 16 wave states of an attention workgroup and its output: the normalised
+// head output converted to the o_proj input (OUT 1: bf16, 2: int8 + group scales), or
+// (OUT 3) the split's partial record (m, l, 0, 0, acc[D]).
+template <int D, int OUT, int SPLIT>
+__device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&acc)[8], int hq, int sp, int num_heads,
+                                            int wave, int krow, int col, int tid, float* s_m, float* s_l, float* s_f,
+                                            float* s_ml, float* s_acc, uint16_t* __restrict__ out_bf16,
+                                            int8_t* __restrict__ out_q, float* __restrict__ out_s,
+                                            float* __restrict__ out_part) {
   using T = AttnTile<D>;
-  constexpr int HALF = D / 2;
-  __shared__ float s_q[D];
-  __shared__ __align__(16) uint16_t s_knew[D];
-  __shared__ __align__(16) uint16_t s_vnew[D];
-  __shared__ float s_m[T::NW], s_l[T::NW], s_f[T::NW], s_ml[2];
-  __shared__ __align__(16) float s_acc[T::NW * D];
-
-  const int G = num_heads / num_kv_heads;
-  // Workgroups are dealt to the 8 XCDs round-robin (XCD = block % 8), each with its own
-  // L2.  With xcd_map the G query heads of one (kv head, split) -- which read the same
-  // K/V rows -- get block ids 8 apart, so they run on one XCD and share its L2.
-  int hq, sp;
-  if (xcd_map) {
-    const int b = blockIdx.x, x = b % 8, j = b / 8;
-    const int pair = (j / G) * 8 + x;  // (kv head, split) pair
-    hq = (pair % num_kv_heads) * G + j % G;
-    sp = pair / num_kv_heads;
-  } else {
-    hq = blockIdx.x % num_heads;
-    sp = blockIdx.x / num_heads;
-  }
-  const int kvh = hq / G;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int col = lane % T::LPK, krow = lane / T::LPK;
-  const size_t cache_base = (size_t)kvh * max_seq * D;
-
-  // three tile buffers in a ring; the first three tiles' loads are issued at once (their
-  // addresses do not depend on the position, rows past the end are masked at use)
-  AttnTile<D> b0, b1, b2;
-  attn_issue<D>(b0, kc, vc, cache_base, sp, max_seq, wave, krow, col);
-  attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, max_seq, wave, krow, col);
-  attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, max_seq, wave, krow, col);
-  // q, k, v of this head before the position-dependent RoPE rows
-  float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
-  if (tid < HALF) {
-    q0 = q[(size_t)hq * D + tid];
-    q1 = q[(size_t)hq * D + tid + HALF];
-    k0 = k[(size_t)kvh * D + tid];
-    k1 = k[(size_t)kvh * D + tid + HALF];
-    v0 = v[(size_t)kvh * D + tid];
-    v1 = v[(size_t)kvh * D + tid + HALF];
-  }
-  // a position past the cache is clamped to its last slot (the host bounds the step
-  // count; the clamp only keeps every access inside the cache and the RoPE tables)
-  const int pos = min(max(*d_pos, 0), max_seq - 1);
-  const int len = pos + 1;
-  const int ntiles = (len + T::KT - 1) / T::KT;
-  // this workgroup's tiles: sp + SPLIT * j for j < nt
-  const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
-
-  if (tid < HALF) {
-    const float c = rope_cos[(size_t)pos * HALF + tid], sn = rope_sin[(size_t)pos * HALF + tid];
-    s_q[tid] = (q0 * c - q1 * sn) * qscale;
-    s_q[tid + HALF] = (q0 * sn + q1 * c) * qscale;
-    s_knew[tid] = f32_to_bf16_bits(k0 * c - k1 * sn);
-    s_knew[tid + HALF] = f32_to_bf16_bits(k0 * sn + k1 * c);
-    s_vnew[tid] = f32_to_bf16_bits(v0);
-    s_vnew[tid + HALF] = f32_to_bf16_bits(v1);
-  }
-  lds_barrier();
-  if (hq % G == 0 && sp == 0)
-    for (int i = tid; i < D; i += 1024) {
-      kc[cache_base + (size_t)pos * D + i] = s_knew[i];
-      vc[cache_base + (size_t)pos * D + i] = s_vnew[i];
-    }
-  float qv[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) qv[e] = s_q[col * 8 + e];
-
-  float m_run = -INFINITY, l_run = 0.0f, acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  // a buffer is refilled only when a later tile of this workgroup remains: loads past
-  // the last tile would only be waited for (their registers are reused by the merge)
-  for (int j = 0; j < nt; j += 3) {
-    attn_compute<D>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
-    if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
-    if (j + 1 < nt)
-      attn_compute<D>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
-    if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
-    if (j + 2 < nt)
-      attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
-    if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
-  }
   // merge the rows of the wave (same columns), then the waves through LDS
   l_run = stride_sum<T::LPK>(l_run);
 #pragma unroll
@@ -315,6 +230,144 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
       q8_group8_store(o, true, out_q, out_s, i0);
     }
   }
+}
+
+// SPLIT > 1 (OUT 3): workgroup (head, sp) takes the tiles t = sp, sp + SPLIT, ... and
+// writes its partial state (m, l, 0, 0, acc[D]) -- m in log2 units, acc not yet
+// divided by l -- to out_part[sp][head]; the consumer merges the SPLIT partials
+// (act_producer.h, SRC_ATTN2 / 4 / 8).  A split with no tile writes m = -inf, l = 0, acc = 0.
+// PRE: the Q/K/V launch has already rotated q (and multiplied it by qscale) and
+// appended the new key and value to the cache (PAIR_ROPE epilogue): q is read as is, the
+// cache holds every row up to pos, and only the first tile's loads are issued before
+// the position is known (the others only if the split has them).
+template <int D, int OUT, int SPLIT = 1, bool PRE = false>
+__global__ __launch_bounds__(1024) void attn_decode_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
+    int max_seq, float qscale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
+    float* __restrict__ out_s, float* __restrict__ out_part, int xcd_map) {
+  static_assert((OUT == 3) == (SPLIT > 1), "split partials go to out_part");
+  using T = AttnTile<D>;
+  constexpr int HALF = D / 2;
+  __shared__ float s_q[D];
+  __shared__ __align__(16) uint16_t s_knew[D];
+  __shared__ __align__(16) uint16_t s_vnew[D];
+  __shared__ float s_m[T::NW], s_l[T::NW], s_f[T::NW], s_ml[2];
+  __shared__ __align__(16) float s_acc[T::NW * D];
+
+  const int G = num_heads / num_kv_heads;
+  // Workgroups are dealt to the 8 XCDs round-robin (XCD = block % 8), each with its own
+  // L2.  With xcd_map the G query heads of one (kv head, split) -- which read the same
+  // K/V rows -- get block ids 8 apart, so they run on one XCD and share its L2.
+  int hq, sp;
+  if (xcd_map) {
+    const int b = blockIdx.x, x = b % 8, j = b / 8;
+    const int pair = (j / G) * 8 + x;  // (kv head, split) pair
+    hq = (pair % num_kv_heads) * G + j % G;
+    sp = pair / num_kv_heads;
+  } else {
+    hq = blockIdx.x % num_heads;
+    sp = blockIdx.x / num_heads;
+  }
+  const int kvh = hq / G;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int col = lane % T::LPK, krow = lane / T::LPK;
+  const size_t cache_base = (size_t)kvh * max_seq * D;
+
+  // three tile buffers in a ring; without PRE the first three tiles' loads are issued at
+  // once (their addresses do not depend on the position, rows past the end are masked
+  // at use); with PRE only the first, and the next two once the position is known
+  AttnTile<D> b0, b1, b2;
+  attn_issue<D>(b0, kc, vc, cache_base, sp, max_seq, wave, krow, col);
+  if (!PRE) {
+    attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, max_seq, wave, krow, col);
+    attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, max_seq, wave, krow, col);
+  }
+  if constexpr (PRE) {
+    const int pos = min(max(*d_pos, 0), max_seq - 1);
+    const int len = pos + 1;
+    const int ntiles = (len + T::KT - 1) / T::KT;
+    const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
+    if (nt > 1) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, len, wave, krow, col);
+    if (nt > 2) attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, len, wave, krow, col);
+    float qv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = q[(size_t)hq * D + col * 8 + e];
+    float m_run = -INFINITY, l_run = 0.0f, acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int j = 0; j < nt; j += 3) {
+      attn_compute<D, false>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
+      if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
+      if (j + 1 < nt)
+        attn_compute<D, false>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                               acc);
+      if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
+      if (j + 2 < nt)
+        attn_compute<D, false>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                               acc);
+      if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
+    }
+    attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_f, s_ml, s_acc,
+                               out_bf16, out_q, out_s, out_part);
+    return;
+  }
+  // q, k, v of this head before the position-dependent RoPE rows
+  float q0 = 0.0f, q1 = 0.0f, k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
+  if (tid < HALF) {
+    q0 = q[(size_t)hq * D + tid];
+    q1 = q[(size_t)hq * D + tid + HALF];
+    k0 = k[(size_t)kvh * D + tid];
+    k1 = k[(size_t)kvh * D + tid + HALF];
+    v0 = v[(size_t)kvh * D + tid];
+    v1 = v[(size_t)kvh * D + tid + HALF];
+  }
+  // a position past the cache is clamped to its last slot (the host bounds the step
+  // count; the clamp only keeps every access inside the cache and the RoPE tables)
+  const int pos = min(max(*d_pos, 0), max_seq - 1);
+  const int len = pos + 1;
+  const int ntiles = (len + T::KT - 1) / T::KT;
+  // this workgroup's tiles: sp + SPLIT * j for j < nt
+  const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
+
+  if (tid < HALF) {
+    const float c = rope_cos[(size_t)pos * HALF + tid], sn = rope_sin[(size_t)pos * HALF + tid];
+    s_q[tid] = (q0 * c - q1 * sn) * qscale;
+    s_q[tid + HALF] = (q0 * sn + q1 * c) * qscale;
+    s_knew[tid] = f32_to_bf16_bits(k0 * c - k1 * sn);
+    s_knew[tid + HALF] = f32_to_bf16_bits(k0 * sn + k1 * c);
+    s_vnew[tid] = f32_to_bf16_bits(v0);
+    s_vnew[tid + HALF] = f32_to_bf16_bits(v1);
+  }
+  lds_barrier();
+  if (hq % G == 0 && sp == 0)
+    for (int i = tid; i < D; i += 1024) {
+      kc[cache_base + (size_t)pos * D + i] = s_knew[i];
+      vc[cache_base + (size_t)pos * D + i] = s_vnew[i];
+    }
+  float qv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) qv[e] = s_q[col * 8 + e];
+
+  float m_run = -INFINITY, l_run = 0.0f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  // a buffer is refilled only when a later tile of this workgroup remains: loads past
+  // the last tile would only be waited for (their registers are reused by the merge)
+  for (int j = 0; j < nt; j += 3) {
+    attn_compute<D>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
+    if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
+    if (j + 1 < nt)
+      attn_compute<D>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
+    if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
+    if (j + 2 < nt)
+      attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
+    if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
+  }
+  attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_f, s_ml, s_acc,
+                             out_bf16, out_q, out_s, out_part);
 }
 
 // ---- SiLU * up ------------------------------------------------------------------
@@ -564,23 +617,28 @@ static hipError_t launch_rmsnorm(const nve_decode_config& c, const float* h, con
   return hipGetLastError();
 }
 
+// pre: the Q/K/V launch ran the PAIR_ROPE epilogue (q rotated and scaled in ws.q, the
+// new key / value already in the cache).
 static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_io& io, const DecodeWs& ws,
-                                   bool w4a8, int split, hipStream_t s) {
+                                   bool w4a8, int split, bool pre, hipStream_t s) {
   // scores in log2 units: q is pre-multiplied by log2(e) / sqrt(D), so the softmax
   // weights are exp2 of score differences
   const float qscale = 1.4426950408889634f / sqrtf((float)c.head_dim);
   // (kv head, split) pairs a multiple of 8: each XCD gets whole groups of query heads
   const int xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1;
-#define NVE_ATTN(D, OUT, S)                                                                                     \
-  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
-                     ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,             \
+#define NVE_ATTN_P(D, OUT, S, P)                                                                             \
+  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S, P>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
+                     ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,                \
                      c.num_kv_heads, c.max_seq, qscale, ws.act_bf16, ws.xq, ws.xs, ws.part, xcd_map)
-#define NVE_ATTN_D(D)                    \
-  if (split == 8) NVE_ATTN(D, 3, 8);     \
-  else if (split == 4) NVE_ATTN(D, 3, 4); \
-  else if (split == 2) NVE_ATTN(D, 3, 2); \
-  else if (w4a8) NVE_ATTN(D, 2, 1);      \
-  else NVE_ATTN(D, 1, 1);
+#define NVE_ATTN(D, OUT, S)          \
+  if (pre) NVE_ATTN_P(D, OUT, S, true); \
+  else NVE_ATTN_P(D, OUT, S, false);
+#define NVE_ATTN_D(D)                      \
+  if (split == 8) { NVE_ATTN(D, 3, 8) }     \
+  else if (split == 4) { NVE_ATTN(D, 3, 4) } \
+  else if (split == 2) { NVE_ATTN(D, 3, 2) } \
+  else if (w4a8) { NVE_ATTN(D, 2, 1) }      \
+  else { NVE_ATTN(D, 1, 1) }
   if (c.head_dim == 64) {
     NVE_ATTN_D(64)
   } else if (c.head_dim == 128) {
@@ -590,6 +648,7 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
   }
 #undef NVE_ATTN_D
 #undef NVE_ATTN
+#undef NVE_ATTN_P
   return hipGetLastError();
 }
 
@@ -622,10 +681,10 @@ static hipError_t gemv(bool w4a8, const DecodeWs& ws, const W4Segs& sg, int out_
               : launch_w4a16(ws.act_bf16, NVE_DT_BF16, sg, out_dt, K, s);
 }
 
-static hipError_t gemv_fused(bool w4a8, int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& sg, int out_dt,
-                             int K, hipStream_t s) {
-  return w4a8 ? launch_w4a8_fused(src, swiglu, pa, sg, out_dt, K, s)
-              : launch_w4a16_fused(src, swiglu, pa, sg, out_dt, K, s);
+static hipError_t gemv_fused(bool w4a8, int src, int pair, const nve::ProdArgs& pa, const W4Segs& sg, int out_dt,
+                             int K, hipStream_t s, const nve::RopeArgs& ra = nve::RopeArgs{}) {
+  return w4a8 ? launch_w4a8_fused(src, pair, pa, sg, out_dt, K, s, ra)
+              : launch_w4a16_fused(src, pair, pa, sg, out_dt, K, s, ra);
 }
 
 // The one-kernel layer (decode_mega.hip) where a compiled tiling fits the shapes, with
@@ -692,8 +751,11 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
     void* outs[3] = {ws.q, ws.k, ws.v};
     const W4Segs sg = segs3(qkv, outs, 3);
     if (fuse) {
-      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, false, nve::ProdArgs{io.hidden, w.input_norm, c.eps}, sg, NVE_DT_F32,
-                         H, s));
+      // RoPE and the KV-cache append run in the epilogue (PAIR_ROPE)
+      const nve::RopeArgs ra{ws.q, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.max_seq,
+                             c.head_dim / 2, 1.4426950408889634f / sqrtf((float)c.head_dim)};
+      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_ROPE, nve::ProdArgs{io.hidden, w.input_norm, c.eps}, sg,
+                         NVE_DT_F32, H, s, ra));
     } else {
       NVE_TRY(launch_rmsnorm(c, io.hidden, w.input_norm, w4a8, ws, s));
       NVE_TRY(gemv(w4a8, ws, sg, NVE_DT_F32, H, s));
@@ -702,9 +764,9 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
   // attention writes the o_proj input directly (int8 + scales, or bf16), or, split over
   // the keys, partials that the o_proj staging merges
   const int split = fuse ? attn_split(c) : 1;
-  NVE_TRY(launch_attention(c, io, ws, w4a8, split, s));
+  NVE_TRY(launch_attention(c, io, ws, w4a8, split, fuse, s));
   if (split > 1)
-    NVE_TRY(gemv_fused(w4a8, split == 8 ? nve::SRC_ATTN8 : (split == 4 ? nve::SRC_ATTN4 : nve::SRC_ATTN2), false,
+    NVE_TRY(gemv_fused(w4a8, split == 8 ? nve::SRC_ATTN8 : (split == 4 ? nve::SRC_ATTN4 : nve::SRC_ATTN2), nve::PAIR_NONE,
                        nve::ProdArgs{ws.part, nullptr, 0.0f, c.head_dim, c.num_heads}, one_seg(w.o, io.hidden),
                        NVE_DT_F32_ACCUM, QD, s));
   else
@@ -717,10 +779,10 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
     if (fuse) {
       void* outs[2] = {w4a8 ? (void*)ws.gate : (void*)ws.act_bf16, nullptr};
       const W4Segs sg = segs3(gu, outs, 2);
-      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, true, nve::ProdArgs{io.hidden, w.post_attn_norm, c.eps}, sg,
+      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_SWIGLU, nve::ProdArgs{io.hidden, w.post_attn_norm, c.eps}, sg,
                          w4a8 ? NVE_DT_F32 : NVE_DT_BF16, H, s));
       if (w4a8)
-        NVE_TRY(gemv_fused(true, nve::SRC_F32, false, nve::ProdArgs{ws.gate, nullptr, 0.0f},
+        NVE_TRY(gemv_fused(true, nve::SRC_F32, nve::PAIR_NONE, nve::ProdArgs{ws.gate, nullptr, 0.0f},
                            one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
       else
         NVE_TRY(gemv(false, ws, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));

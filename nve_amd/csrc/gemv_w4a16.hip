@@ -38,15 +38,17 @@ namespace nve {
 
 // SRC != SRC_PLAIN (MODE_BF16 only): the activations are computed in the staging
 // from the producer's inputs (act_producer.h) and rounded to bf16.
-// SWI: SwiGLU pairing -- segment 0 (gate) and the matrix in nib[1] / sc[1] (up)
-// share N; a wave computes R/2 rows of each and writes silu(gate) * up
-// (src/ops.rs:62-64) for its R/2 rows.
-template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, bool SWI = false>
+// PAIR (act_producer.h): PAIR_SWIGLU -- segment 0 (gate) and the matrix in nib[1] /
+// sc[1] (up) share N; a wave computes R/2 rows of each and writes silu(gate) * up
+// (src/ops.rs:62-64).  PAIR_ROPE -- segments q, k, v, each N = rows / 2 pairs; a wave
+// computes both rows of R/2 RoPE pairs and writes the attention's input (rope_store).
+template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, int PAIR = PAIR_NONE>
 __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict__ x, W4Segs segs,
-                                                         int K, ProdArgs pa) {
+                                                         int K, ProdArgs pa, RopeArgs ra) {
+  constexpr bool SWI = PAIR == PAIR_SWIGLU, ROPE = PAIR == PAIR_ROPE;
   static_assert(SRC == SRC_PLAIN || (!MULTI && MODE == MODE_BF16), "fused producers: one-pass bf16 staging");
-  static_assert(!SWI || (R % 2 == 0 && !MULTI && MODE != MODE_F32), "SwiGLU pairing: even R, one pass");
-  constexpr int RH = SWI ? R / 2 : R;  // output rows per wave
+  static_assert(PAIR == PAIR_NONE || (R % 2 == 0 && !MULTI && MODE != MODE_F32), "paired rows: even R, one pass");
+  constexpr int RH = PAIR != PAIR_NONE ? R / 2 : R;  // output rows (pairs) per wave
   constexpr int SPT = NJ;  // staging passes: K/8 chunks <= 256*NJ
   extern __shared__ int4 lds[];
   const int nb = K >> 5;
@@ -101,7 +103,8 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   auto issue = [&](int jb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + (SWI ? r % RH : r), N - 1);
+      const int rr = min(row0 + (PAIR != PAIR_NONE ? r % RH : r), N - 1);
+      const int row = ROPE ? rope_row(rr, ra.half, r >= RH) : rr;
       const uint8_t* mn = (SWI && r >= RH) ? segs.nib[1] : nib;
       const float* ms = (SWI && r >= RH) ? segs.sc[1] : ws;
       const uint4* rn = (const uint4*)(mn + (size_t)row * row_bytes);
@@ -115,6 +118,18 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
     }
   };
   issue(0);
+  // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
+  int rpos = 0;
+  float rc[ROPE ? RH : 1], rs[ROPE ? RH : 1];
+  if constexpr (ROPE) {
+    rpos = rope_pos(ra);
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const int d = min(row0 + r, N - 1) % ra.half;
+      rc[r] = ra.cos[(size_t)rpos * ra.half + d];
+      rs[r] = ra.sin[(size_t)rpos * ra.half + d];
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // (3) LDS writes
@@ -187,6 +202,13 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       const float u = wave_sum_to_lane63(acc[r + RH]);
       if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), g / (1.0f + expf(-g)) * u);
     }
+  } else if constexpr (ROPE) {
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const float x0 = wave_sum_to_lane63(acc[r]);
+      const float x1 = wave_sum_to_lane63(acc[r + RH]);
+      if (lane == 63 && row0 + r < N) rope_store(ra, sg, row0 + r, x0, x1, rc[r], rs[r], rpos);
+    }
   } else {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -203,16 +225,17 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
 // ---------------------------------------------------------------------------
 namespace nve_host {
 
-template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = nve::SRC_PLAIN, bool SWI = false>
+template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = nve::SRC_PLAIN,
+          int PAIR = nve::PAIR_NONE>
 static hipError_t launch_w4a16_t(const void* x, const W4Segs& segs, int K, hipStream_t stream,
-                                 const nve::ProdArgs& pa = nve::ProdArgs{}) {
+                                 const nve::ProdArgs& pa = nve::ProdArgs{}, const nve::RopeArgs& ra = nve::RopeArgs{}) {
   const size_t lds = nve::w4a16_lds_bytes(MODE, K) + (SRC == nve::SRC_NORM ? 64 : 0);
-  auto kern = nve::w4a16_gemv_kernel<MODE, XDT, OUT_DT, R, NJ, MULTI, SRC, SWI>;
+  auto kern = nve::w4a16_gemv_kernel<MODE, XDT, OUT_DT, R, NJ, MULTI, SRC, PAIR>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(segs.wg_total), dim3(256), lds, stream, x, segs, K, pa);
+  hipLaunchKernelGGL(kern, dim3(segs.wg_total), dim3(256), lds, stream, x, segs, K, pa, ra);
   return hipGetLastError();
 }
 
@@ -228,19 +251,22 @@ static hipError_t launch_w4a16_m(const void* x, W4Segs segs, int K, hipStream_t 
   return hipErrorInvalidValue;
 }
 
-template <int OUT_DT, int SRC, bool SWI>
-static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream) {
+template <int OUT_DT, int SRC, int PAIR>
+static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream,
+                                       const nve::RopeArgs& ra) {
   const W4Tiling t = nve::attn_splits_of(SRC) ? choose_merge_tiling(segs, K) : choose_w4_tiling(segs, K);
   if (t.multi) return hipErrorInvalidValue;
-  if (SWI) {
+  if (PAIR != nve::PAIR_NONE) {
     const int R = t.R < 2 ? 2 : t.R;
-    segs.nseg = 1;  // gate in slot 0, up in slot 1 (read by the kernel directly)
+    if (PAIR == nve::PAIR_SWIGLU) segs.nseg = 1;  // gate in slot 0, up in slot 1 (read by the kernel directly)
+    if (PAIR == nve::PAIR_ROPE)
+      for (int i = 0; i < segs.nseg; ++i) segs.n[i] /= 2;  // RoPE pairs per matrix
     finalize_segments(segs, R / 2);
-#define NVE_W4A16_SWI_CASE(RR, JJ) \
+#define NVE_W4A16_PAIR_CASE(RR, JJ) \
     if (R == RR && t.NJ == JJ) \
-      return launch_w4a16_t<nve::MODE_BF16, NVE_DT_BF16, OUT_DT, RR, JJ, false, SRC, true>(nullptr, segs, K, stream, pa);
-    NVE_W4_SWIGLU_CASES(NVE_W4A16_SWI_CASE)
-#undef NVE_W4A16_SWI_CASE
+      return launch_w4a16_t<nve::MODE_BF16, NVE_DT_BF16, OUT_DT, RR, JJ, false, SRC, PAIR>(nullptr, segs, K, stream, pa, ra);
+    NVE_W4_SWIGLU_CASES(NVE_W4A16_PAIR_CASE)
+#undef NVE_W4A16_PAIR_CASE
     return hipErrorInvalidValue;
   }
   finalize_segments(segs, t.R);
@@ -280,21 +306,23 @@ hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt,
 }
 
 // Decode-layer W4A16 GEMVs with a fused producer (act_producer.h), bf16 staging:
+//   NORM, F32, rope    Q/K/V from the residual and the norm weights, RoPE + KV append
+//                      in the epilogue (PAIR_ROPE);
 //   NORM, F32          Q/K/V from the residual and the norm weights;
 //   NORM, BF16, swiglu gate/up -> silu(gate) * up rounded to bf16 (the down input);
 //   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
-hipError_t launch_w4a16_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                              hipStream_t stream) {
-  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && !swiglu)
-    return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, false>(pa, segs, K, stream);
-  if (src == nve::SRC_NORM && out_dt == NVE_DT_BF16 && swiglu)
-    return launch_w4a16_fused_t<NVE_DT_BF16, nve::SRC_NORM, true>(pa, segs, K, stream);
-  if (src == nve::SRC_ATTN2 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
-    return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, false>(pa, segs, K, stream);
-  if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
-    return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, false>(pa, segs, K, stream);
-  if (src == nve::SRC_ATTN8 && out_dt == NVE_DT_F32_ACCUM && !swiglu)
-    return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN8, false>(pa, segs, K, stream);
+hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                              hipStream_t stream, const nve::RopeArgs& ra) {
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && pair == nve::PAIR_ROPE)
+    return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_ROPE>(pa, segs, K, stream, ra);
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && pair == nve::PAIR_NONE)
+    return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_NONE>(pa, segs, K, stream, ra);
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_BF16 && pair == nve::PAIR_SWIGLU)
+    return launch_w4a16_fused_t<NVE_DT_BF16, nve::SRC_NORM, nve::PAIR_SWIGLU>(pa, segs, K, stream, ra);
+  if (pair != nve::PAIR_NONE || out_dt != NVE_DT_F32_ACCUM) return hipErrorInvalidValue;
+  if (src == nve::SRC_ATTN2) return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, nve::PAIR_NONE>(pa, segs, K, stream, ra);
+  if (src == nve::SRC_ATTN4) return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, nve::PAIR_NONE>(pa, segs, K, stream, ra);
+  if (src == nve::SRC_ATTN8) return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN8, nve::PAIR_NONE>(pa, segs, K, stream, ra);
   return hipErrorInvalidValue;
 }
 

@@ -36,16 +36,18 @@ namespace nve {
 // than one pass of NJ chunks (K > 64*NJ*32); then staging runs as a loop.  SRC !=
 // SRC_PLAIN computes the activations in the staging from the producer's inputs
 // (act_producer.h) and quantizes them in place of reading xq / xs.
-// SWI: SwiGLU pairing -- segment 0 (gate) and the matrix in nib[1] / sc[1] (up)
-// share N; a wave computes R/2 rows of each and writes silu(gate) * up
-// (src/ops.rs:62-64) for its R/2 rows.
-template <int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, bool SWI = false>
+// PAIR (act_producer.h): PAIR_SWIGLU -- segment 0 (gate) and the matrix in nib[1] /
+// sc[1] (up) share N; a wave computes R/2 rows of each and writes silu(gate) * up
+// (src/ops.rs:62-64).  PAIR_ROPE -- segments q, k, v, each N = rows / 2 pairs; a wave
+// computes both rows of R/2 RoPE pairs and writes the attention's input (rope_store).
+template <int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, int PAIR = PAIR_NONE>
 __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xs,
-                                                        W4Segs segs, int K, ProdArgs pa) {
+                                                        W4Segs segs, int K, ProdArgs pa, RopeArgs ra) {
+  constexpr bool SWI = PAIR == PAIR_SWIGLU, ROPE = PAIR == PAIR_ROPE;
   static_assert(SRC == SRC_PLAIN || !MULTI, "fused producers stage in one pass");
-  static_assert(!SWI || (R % 2 == 0 && !MULTI), "SwiGLU pairing: even R, one pass");
-  constexpr int RH = SWI ? R / 2 : R;  // output rows per wave
+  static_assert(PAIR == PAIR_NONE || (R % 2 == 0 && !MULTI), "paired rows: even R, one pass");
+  constexpr int RH = PAIR != PAIR_NONE ? R / 2 : R;  // output rows (pairs) per wave
   constexpr int SPT = (NJ + 1) / 2;  // staging passes: 2*nb <= 128*NJ chunks of 16 B
   extern __shared__ int4 lds[];
   const int nb = K >> 5;
@@ -86,7 +88,8 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   auto issue = [&](int jb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + (SWI ? r % RH : r), N - 1);
+      const int rr = min(row0 + (PAIR != PAIR_NONE ? r % RH : r), N - 1);
+      const int row = ROPE ? rope_row(rr, ra.half, r >= RH) : rr;
       const uint8_t* mn = (SWI && r >= RH) ? segs.nib[1] : nib;
       const float* ms = (SWI && r >= RH) ? segs.sc[1] : ws;
       const uint4* rn = (const uint4*)(mn + (size_t)row * row_bytes);
@@ -101,6 +104,18 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     }
   };
   issue(0);
+  // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
+  int rpos = 0;
+  float rc[ROPE ? RH : 1], rs[ROPE ? RH : 1];
+  if constexpr (ROPE) {
+    rpos = rope_pos(ra);
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const int d = min(row0 + r, N - 1) % ra.half;
+      rc[r] = ra.cos[(size_t)rpos * ra.half + d];
+      rs[r] = ra.sin[(size_t)rpos * ra.half + d];
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (SRC != SRC_PLAIN) {
@@ -157,6 +172,13 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       const float u = wave_sum_to_lane63(acc[r + RH]);
       if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), g / (1.0f + expf(-g)) * u);
     }
+  } else if constexpr (ROPE) {
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const float x0 = wave_sum_to_lane63(acc[r]);
+      const float x1 = wave_sum_to_lane63(acc[r + RH]);
+      if (lane == 63 && row0 + r < N) rope_store(ra, sg, row0 + r, x0, x1, rc[r], rs[r], rpos);
+    }
   } else {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -190,16 +212,17 @@ __global__ __launch_bounds__(256) void w4a8_block_acc_kernel(const int8_t* __res
 // ---------------------------------------------------------------------------
 namespace nve_host {
 
-template <int OUT_DT, int R, int NJ, bool MULTI, int SRC, bool SWI>
+template <int OUT_DT, int R, int NJ, bool MULTI, int SRC, int PAIR>
 static hipError_t launch_w4a8_t(const int8_t* xq, const float* xs, const W4Segs& segs, int K,
-                                int grid, const nve::ProdArgs& pa, hipStream_t stream) {
+                                int grid, const nve::ProdArgs& pa, hipStream_t stream,
+                                const nve::RopeArgs& ra = nve::RopeArgs{}) {
   const size_t lds = nve::w4a8_lds_bytes(K) + (SRC == nve::SRC_NORM ? 64 : 0);
-  auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI, SRC, SWI>;
+  auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI, SRC, PAIR>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, xq, xs, segs, K, pa);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, xq, xs, segs, K, pa, ra);
   return hipGetLastError();
 }
 
@@ -211,32 +234,35 @@ static hipError_t launch_w4a8_dt(const int8_t* xq, const float* xs, W4Segs segs,
   const int grid = segs.wg_total;
 #define NVE_W4A8_CASE(RR, JJ, MM) \
   if (t.R == RR && t.NJ == JJ && t.multi == MM) \
-    return launch_w4a8_t<OUT_DT, RR, JJ, MM, nve::SRC_PLAIN, false>(xq, xs, segs, K, grid, nve::ProdArgs{}, stream);
+    return launch_w4a8_t<OUT_DT, RR, JJ, MM, nve::SRC_PLAIN, nve::PAIR_NONE>(xq, xs, segs, K, grid, nve::ProdArgs{}, stream);
   NVE_W4_TILING_CASES(NVE_W4A8_CASE)
 #undef NVE_W4A8_CASE
   return hipErrorInvalidValue;
 }
 
 // Fused-producer launches (one-shot kernels, one staging pass: K <= 16384).
-template <int OUT_DT, int SRC, bool SWI>
-static hipError_t launch_w4a8_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream) {
+template <int OUT_DT, int SRC, int PAIR>
+static hipError_t launch_w4a8_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream,
+                                      const nve::RopeArgs& ra) {
   const W4Tiling t = nve::attn_splits_of(SRC) ? choose_merge_tiling(segs, K) : choose_w4_tiling(segs, K);
   if (t.multi) return hipErrorInvalidValue;
-  if (SWI) {
+  if (PAIR != nve::PAIR_NONE) {
     const int R = t.R < 2 ? 2 : t.R;
-    segs.nseg = 1;  // gate in slot 0, up in slot 1 (read by the kernel directly)
+    if (PAIR == nve::PAIR_SWIGLU) segs.nseg = 1;  // gate in slot 0, up in slot 1 (read by the kernel directly)
+    if (PAIR == nve::PAIR_ROPE)
+      for (int i = 0; i < segs.nseg; ++i) segs.n[i] /= 2;  // RoPE pairs per matrix
     finalize_segments(segs, R / 2);
-#define NVE_W4A8_SWI_CASE(RR, JJ) \
+#define NVE_W4A8_PAIR_CASE(RR, JJ) \
     if (R == RR && t.NJ == JJ) \
-      return launch_w4a8_t<OUT_DT, RR, JJ, false, SRC, true>(nullptr, nullptr, segs, K, segs.wg_total, pa, stream);
-    NVE_W4_SWIGLU_CASES(NVE_W4A8_SWI_CASE)
-#undef NVE_W4A8_SWI_CASE
+      return launch_w4a8_t<OUT_DT, RR, JJ, false, SRC, PAIR>(nullptr, nullptr, segs, K, segs.wg_total, pa, stream, ra);
+    NVE_W4_SWIGLU_CASES(NVE_W4A8_PAIR_CASE)
+#undef NVE_W4A8_PAIR_CASE
     return hipErrorInvalidValue;
   }
   finalize_segments(segs, t.R);
 #define NVE_W4A8_CASE(RR, JJ, MM) \
   if (t.R == RR && t.NJ == JJ && !MM) \
-    return launch_w4a8_t<OUT_DT, RR, JJ, false, SRC, false>(nullptr, nullptr, segs, K, segs.wg_total, pa, stream);
+    return launch_w4a8_t<OUT_DT, RR, JJ, false, SRC, nve::PAIR_NONE>(nullptr, nullptr, segs, K, segs.wg_total, pa, stream);
   NVE_W4_TILING_CASES(NVE_W4A8_CASE)
 #undef NVE_W4A8_CASE
   return hipErrorInvalidValue;
@@ -254,35 +280,38 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
 }
 
 // Decode-layer W4A8 GEMVs with a fused producer (act_producer.h):
+//   NORM, F32, rope    Q/K/V from the residual and the norm weights, RoPE + KV append
+//                      in the epilogue (PAIR_ROPE; out[] unused);
 //   NORM, F32          Q/K/V from the residual and the norm weights;
 //   NORM, F32, swiglu  gate/up -> silu(gate) * up (f32);
 //   F32, F32_ACCUM     down from that f32 vector, quantized in the staging;
 //   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
-hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                             hipStream_t stream) {
-  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32)
-    return swiglu ? launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, true>(pa, segs, K, stream)
-                  : launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, false>(pa, segs, K, stream);
-  if (swiglu) return hipErrorInvalidValue;
-  if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM)
-    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_F32, false>(pa, segs, K, stream);
-  if (src == nve::SRC_ATTN2 && out_dt == NVE_DT_F32_ACCUM)
-    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, false>(pa, segs, K, stream);
-  if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM)
-    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, false>(pa, segs, K, stream);
-  if (src == nve::SRC_ATTN8 && out_dt == NVE_DT_F32_ACCUM)
-    return launch_w4a8_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN8, false>(pa, segs, K, stream);
+hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                             hipStream_t stream, const nve::RopeArgs& ra) {
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F32) {
+    if (pair == nve::PAIR_ROPE)
+      return launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_ROPE>(pa, segs, K, stream, ra);
+    return pair == nve::PAIR_SWIGLU ? launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_SWIGLU>(pa, segs, K, stream, ra)
+                                    : launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_NONE>(pa, segs, K, stream, ra);
+  }
+  if (pair != nve::PAIR_NONE) return hipErrorInvalidValue;
+#define NVE_FU(SRC, OD) launch_w4a8_fused_t<OD, SRC, nve::PAIR_NONE>(pa, segs, K, stream, ra)
+  if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_F32, NVE_DT_F32_ACCUM);
+  if (src == nve::SRC_ATTN2 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_ATTN2, NVE_DT_F32_ACCUM);
+  if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_ATTN4, NVE_DT_F32_ACCUM);
+  if (src == nve::SRC_ATTN8 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_ATTN8, NVE_DT_F32_ACCUM);
   // W4A8 GEMV quantizing its own 16-bit / f32 activations (fp16 or fp32 output)
 #define NVE_QX(SRC)                                                                    \
   if (src == SRC) {                                                                    \
-    if (out_dt == NVE_DT_F16) return launch_w4a8_fused_t<NVE_DT_F16, SRC, false>(pa, segs, K, stream); \
-    if (out_dt == NVE_DT_F32) return launch_w4a8_fused_t<NVE_DT_F32, SRC, false>(pa, segs, K, stream); \
+    if (out_dt == NVE_DT_F16) return NVE_FU(SRC, NVE_DT_F16);                          \
+    if (out_dt == NVE_DT_F32) return NVE_FU(SRC, NVE_DT_F32);                          \
     return hipErrorInvalidValue;                                                       \
   }
   NVE_QX(nve::SRC_F16)
   NVE_QX(nve::SRC_BF16)
   NVE_QX(nve::SRC_F32)
 #undef NVE_QX
+#undef NVE_FU
   return hipErrorInvalidValue;
 }
 

@@ -186,17 +186,18 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
 int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8, hipStream_t s);
 int layer_forward_decode_noalloc(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                                  bool w4a8, hipStream_t s);
-// Fused-producer GEMVs (act_producer.h); swiglu pairs gate (slot 0) with up (nib[1],
-// sc[1]) and writes silu(gate) * up.
+// Fused-producer GEMVs (act_producer.h).
 }  // namespace nve_host
 namespace nve {
 struct ProdArgs;
+struct RopeArgs;
 }
 namespace nve_host {
-hipError_t launch_w4a8_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                             hipStream_t stream);
-hipError_t launch_w4a16_fused(int src, bool swiglu, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                              hipStream_t stream);
+// pair: nve::PAIR_NONE / PAIR_SWIGLU / PAIR_ROPE (act_producer.h); ra is read by PAIR_ROPE only.
+hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                             hipStream_t stream, const nve::RopeArgs& ra);
+hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
+                              hipStream_t stream, const nve::RopeArgs& ra);
 hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);
