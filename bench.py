@@ -395,7 +395,7 @@ def batched_sweep(torch, L, weights, launches_per_graph: int = 40):
             rec = {"M": m, "N": n, "K": k, "us": round(us, 3), "GBs": round(b / us / 1e3, 1),
                    "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                    "useful_int8_TOPs": round(2 * m * n * k / us / 1e6, 2),
-                   "kernel": "mfma_i32_16x16x32_i8" if m >= 2 else "v_dot4"}
+                   "kernel": "mfma_i32_16x16x32_i8" if m >= 2 else "w4a8_gemv (one-shot, v_dot4)"}
             if m >= 2:
                 issued = 2 * 16 * n * k / us / 1e6
                 rec["issued_mfma_TOPs"] = round(issued, 2)

@@ -43,6 +43,10 @@ struct ProdArgs {
   const void* b;
   float eps;
   int i0, i1;
+  // SRC_PLAIN W4A8 only: one bf16 activation scale for the whole row (per-token mode);
+  // the block sums are then formed with the weight scales alone and the row sum is
+  // multiplied by this scale (NULL: group-32 scales from xs).
+  const uint16_t* row_scale;
 };
 
 // E activations (8 or 16) of one staging chunk: f32 sources in a, 16-bit sources in h.

@@ -286,15 +286,19 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, max_seq, wave, krow, col);
   }
   if constexpr (PRE) {
+    // q (rotated, scaled) is loaded with the first tile, before the position
+    float qv[8];
+    {
+      const float4 qa = *(const float4*)(q + (size_t)hq * D + col * 8);
+      const float4 qb = *(const float4*)(q + (size_t)hq * D + col * 8 + 4);
+      qv[0] = qa.x, qv[1] = qa.y, qv[2] = qa.z, qv[3] = qa.w, qv[4] = qb.x, qv[5] = qb.y, qv[6] = qb.z, qv[7] = qb.w;
+    }
     const int pos = min(max(*d_pos, 0), max_seq - 1);
     const int len = pos + 1;
     const int ntiles = (len + T::KT - 1) / T::KT;
     const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
     if (nt > 1) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, len, wave, krow, col);
     if (nt > 2) attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, len, wave, krow, col);
-    float qv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qv[e] = q[(size_t)hq * D + col * 8 + e];
     float m_run = -INFINITY, l_run = 0.0f, acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;

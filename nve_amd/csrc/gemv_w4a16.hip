@@ -117,7 +117,9 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       }
     }
   };
-  issue(0);
+  // SRC_NORM: weight loads issued once the norm statistic is known (see gemv_w4a8.hip)
+  constexpr bool kLateWeights = SRC == SRC_NORM;
+  if (!kLateWeights) issue(0);
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
   int rpos = 0;
   float rc[ROPE ? RH : 1], rs[ROPE ? RH : 1];
@@ -138,6 +140,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
     if (SRC == SRC_NORM)
       inv = prod_norm_inv(prod_sumsq<SRC, 8, SPT>(pc, nchunk), K, pa.eps,
                           (double*)((char*)lds + w4a16_lds_bytes(MODE, K)));
+    if (kLateWeights) issue(0);
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;

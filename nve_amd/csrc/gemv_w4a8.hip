@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
 #pragma unroll
     for (int s = 0; s < SPT; ++s) prod_issue<SRC, 16>(pc[s], pa, (int)threadIdx.x + 256 * s, nchunk);
   } else if (!MULTI) {
-    w4a8_stage_issue<SPT>(st, xq, xs, nchunk);
+    w4a8_stage_issue<SPT>(st, xq, xs, nchunk, pa.row_scale != nullptr);
   }
   // Keep the issue order: staging loads, then weight loads, then LDS writes (which
   // then wait only for the older staging loads).
@@ -103,7 +103,15 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       }
     }
   };
-  issue(0);
+  // With the RMSNorm in the staging (SRC_NORM) the weight loads are issued once the norm
+  // statistic is known: the residual was just written by the previous launch and is
+  // fetched past the L2, and issued beside this launch's whole weight stream its loads
+  // return late (timestamps in the gate/up launch of the 3B decode step: the norm
+  // statistic at 3.8 us median with the weights issued first, 2.0 us with them issued
+  // after it, kernel end 7.4 -> 6.6 us).  Other fused producers keep the early issue
+  // (issuing late after their staging was measured slower).
+  constexpr bool kLateWeights = SRC == SRC_NORM;
+  if (!kLateWeights) issue(0);
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
   int rpos = 0;
   float rc[ROPE ? RH : 1], rs[ROPE ? RH : 1];
@@ -123,6 +131,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     if (SRC == SRC_NORM)
       inv = prod_norm_inv(prod_sumsq<SRC, 16, SPT>(pc, nchunk), K, pa.eps,
                           (double*)((char*)lds + w4a8_lds_bytes(K)));
+    if (kLateWeights) issue(0);
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;
@@ -135,7 +144,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   } else if (!MULTI) {
     w4a8_stage_write<SPT>(st, s_lo, s_hi, s_bs, nchunk);
   } else {
-    w4a8_stage_loop(xq, xs, s_lo, s_hi, s_bs, nchunk);
+    w4a8_stage_loop(xq, xs, s_lo, s_hi, s_bs, nchunk, pa.row_scale != nullptr);
   }
   lds_barrier();
 
@@ -180,9 +189,11 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       if (lane == 63 && row0 + r < N) rope_store(ra, sg, row0 + r, x0, x1, rc[r], rs[r], rpos);
     }
   } else {
+    const float rsc = (SRC == SRC_PLAIN && pa.row_scale) ? bf16_bits_to_f32(*pa.row_scale) : 1.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const float v = wave_sum_to_lane63(acc[r]);
+      float v = wave_sum_to_lane63(acc[r]);
+      if (SRC == SRC_PLAIN && pa.row_scale) v *= rsc;
       if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
     }
   }
@@ -228,13 +239,13 @@ static hipError_t launch_w4a8_t(const int8_t* xq, const float* xs, const W4Segs&
 
 template <int OUT_DT>
 static hipError_t launch_w4a8_dt(const int8_t* xq, const float* xs, W4Segs segs, int K,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const nve::ProdArgs& pa = nve::ProdArgs{}) {
   const W4Tiling t = choose_w4_tiling(segs, K);
   finalize_segments(segs, t.R);
   const int grid = segs.wg_total;
 #define NVE_W4A8_CASE(RR, JJ, MM) \
   if (t.R == RR && t.NJ == JJ && t.multi == MM) \
-    return launch_w4a8_t<OUT_DT, RR, JJ, MM, nve::SRC_PLAIN, nve::PAIR_NONE>(xq, xs, segs, K, grid, nve::ProdArgs{}, stream);
+    return launch_w4a8_t<OUT_DT, RR, JJ, MM, nve::SRC_PLAIN, nve::PAIR_NONE>(xq, xs, segs, K, grid, pa, stream);
   NVE_W4_TILING_CASES(NVE_W4A8_CASE)
 #undef NVE_W4A8_CASE
   return hipErrorInvalidValue;
@@ -266,6 +277,21 @@ static hipError_t launch_w4a8_fused_t(const nve::ProdArgs& pa, W4Segs segs, int 
   NVE_W4_TILING_CASES(NVE_W4A8_CASE)
 #undef NVE_W4A8_CASE
   return hipErrorInvalidValue;
+}
+
+// One activation row with one bf16 scale (per-token mode, the M = 1 case of the batched
+// entry point): the one-shot kernel with unit block scales and the row scale applied to
+// the row sums.
+hipError_t launch_w4a8_rowscale(const int8_t* xq, const uint16_t* row_scale, const W4Segs& segs, int out_dt, int K,
+                                hipStream_t stream) {
+  nve::ProdArgs pa{};
+  pa.row_scale = row_scale;
+  const float* no_xs = nullptr;
+  switch (out_dt) {
+    case NVE_DT_F16: return launch_w4a8_dt<NVE_DT_F16>(xq, no_xs, segs, K, stream, pa);
+    case NVE_DT_BF16: return launch_w4a8_dt<NVE_DT_BF16>(xq, no_xs, segs, K, stream, pa);
+    default: return launch_w4a8_dt<NVE_DT_F32>(xq, no_xs, segs, K, stream, pa);
+  }
 }
 
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,

@@ -5,7 +5,8 @@
 // or the per-row bf16 scale (per-token mode, applied once per row: the sum over
 // blocks is formed with ws only and multiplied by the row scale at the end).
 //
-// v_dot4 kernel (M = 1, or any M under NVE_GEMV_ONESHOT): one wave per output row, lane l owns
+// M = 1 runs the one-shot W4A8 GEMV (gemv_w4a8.hip).
+// v_dot4 kernel (any M >= 2 under NVE_GEMV_ONESHOT): one wave per output row, lane l owns
 // blocks l, l+64, ...; the nibbles are turned into signed int8 (nib - 8) once per
 // block with (t + 0x78787878) ^ 0x80808080 (no carries cross bytes for t <= 15), and
 // every activation row reuses them through 8 v_dot4_i32_i8.
@@ -288,7 +289,19 @@ template <int OUT_DT>
 static hipError_t launch_batched_o(int M, const int8_t* xq, const void* xs, int xs_mode,
                                    const uint8_t* nib, const float* ws, void* out, int N, int K,
                                    hipStream_t stream) {
-  if (M >= 2 && batched_use_mfma()) {
+  if (M == 1) {
+    // one row: the one-shot GEMV (its staged activations and per-lane block order), with
+    // the row's bf16 scale applied to the row sums in per-token mode
+    W4Segs s{};
+    s.nseg = 1;
+    s.nib[0] = nib;
+    s.sc[0] = ws;
+    s.out[0] = out;
+    s.n[0] = N;
+    if (xs_mode == NVE_XS_ROW_BF16) return launch_w4a8_rowscale(xq, (const uint16_t*)xs, s, OUT_DT, K, stream);
+    return launch_w4a8(xq, (const float*)xs, s, OUT_DT, K, stream);
+  }
+  if (batched_use_mfma()) {
     if (xs_mode == NVE_XS_ROW_BF16)
       return launch_mfma_m<OUT_DT, NVE_XS_ROW_BF16>(M, xq, xs, nib, ws, out, N, K, stream);
     return launch_mfma_m<OUT_DT, NVE_XS_GROUP32_F32>(M, xq, xs, nib, ws, out, N, K, stream);

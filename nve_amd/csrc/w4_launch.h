@@ -201,6 +201,8 @@ hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const 
 hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);
+hipError_t launch_w4a8_rowscale(const int8_t* xq, const uint16_t* row_scale, const W4Segs& segs, int out_dt, int K,
+                                hipStream_t stream);
 hipError_t launch_w4a8_block_acc(const int8_t* xq, const uint8_t* nib, int32_t* acc, int N, int K,
                                  hipStream_t stream);
 hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt, int K,

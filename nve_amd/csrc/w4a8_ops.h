@@ -50,14 +50,16 @@ struct W4A8Stage {
   float xs[SPT];
 };
 
+// xs_one: every block scale is 1 (the per-token mode applies one row scale at the end);
+// xs is not read.
 template <int SPT>
 __device__ __forceinline__ void w4a8_stage_issue(W4A8Stage<SPT>& st, const int8_t* __restrict__ xq,
-                                                 const float* __restrict__ xs, int nchunk) {
+                                                 const float* __restrict__ xs, int nchunk, bool xs_one = false) {
 #pragma unroll
   for (int s = 0; s < SPT; ++s) {
     const int i = min((int)threadIdx.x + 256 * s, nchunk - 1);
     st.v[s] = ((const int4*)xq)[i];
-    st.xs[s] = xs[i >> 1];
+    st.xs[s] = xs_one ? 1.0f : xs[i >> 1];
   }
 }
 
@@ -87,11 +89,11 @@ __device__ __forceinline__ void w4a8_stage_write(const W4A8Stage<SPT>& st, int4*
 // Staging for K > 16384 (MULTI kernels): loads and LDS writes in one loop.
 __device__ __forceinline__ void w4a8_stage_loop(const int8_t* __restrict__ xq,
                                                 const float* __restrict__ xs, int4* s_lo,
-                                                int4* s_hi, int2* s_bs, int nchunk) {
+                                                int4* s_hi, int2* s_bs, int nchunk, bool xs_one = false) {
   for (int base = 0; base < nchunk; base += 256) {
     const int i = base + threadIdx.x;
     const int ic = min(i, nchunk - 1);
-    w4a8_stage_put(((const int4*)xq)[ic], xs[ic >> 1], i, i < nchunk, nchunk >> 1, s_lo, s_hi,
+    w4a8_stage_put(((const int4*)xq)[ic], xs_one ? 1.0f : xs[ic >> 1], i, i < nchunk, nchunk >> 1, s_lo, s_hi,
                    s_bs);
   }
 }
