@@ -117,8 +117,9 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       }
     }
   };
-  // SRC_NORM: weight loads issued once the norm statistic is known (see gemv_w4a8.hip)
-  constexpr bool kLateWeights = SRC == SRC_NORM;
+  // SRC_NORM / SRC_F32: weight loads issued once the norm statistic is known / the vector
+  // is staged (see gemv_w4a8.hip)
+  constexpr bool kLateWeights = SRC == SRC_NORM || SRC == SRC_F32;
   if (!kLateWeights) issue(0);
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
   int rpos = 0;
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
     if (SRC == SRC_NORM)
       inv = prod_norm_inv(prod_sumsq<SRC, 8, SPT>(pc, nchunk), K, pa.eps,
                           (double*)((char*)lds + w4a16_lds_bytes(MODE, K)));
-    if (kLateWeights) issue(0);
+    if (kLateWeights && SRC == SRC_NORM) issue(0);
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;
@@ -148,6 +149,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       prod_values<SRC, 8>(pc[s], inv, v);
       w4a16_stage_put_dot<MODE>(prod_bf16x8(v), i, i < nchunk, nb, s_p, s_mul);
     }
+    if (kLateWeights && SRC != SRC_NORM) issue(0);
   } else if (!MULTI) {
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {

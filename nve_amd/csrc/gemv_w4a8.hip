@@ -104,13 +104,13 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     }
   };
   // With the RMSNorm in the staging (SRC_NORM) the weight loads are issued once the norm
-  // statistic is known: the residual was just written by the previous launch and is
-  // fetched past the L2, and issued beside this launch's whole weight stream its loads
-  // return late (timestamps in the gate/up launch of the 3B decode step: the norm
-  // statistic at 3.8 us median with the weights issued first, 2.0 us with them issued
-  // after it, kernel end 7.4 -> 6.6 us).  Other fused producers keep the early issue
-  // (issuing late after their staging was measured slower).
-  constexpr bool kLateWeights = SRC == SRC_NORM;
+  // statistic is known, and with an f32 producer vector (SRC_F32) once it is staged: the
+  // vector was just written by the previous launch and is fetched past the L2, and
+  // issued beside this launch's whole weight stream its loads return late (timestamps in
+  // the gate/up launch of the 3B decode step: the norm statistic at 3.8 us median with
+  // the weights issued first, 2.0 us with them issued after it, kernel end 7.4 -> 6.6
+  // us).  The attention-merge producers keep the early issue (late was measured slower).
+  constexpr bool kLateWeights = SRC == SRC_NORM || SRC == SRC_F32;
   if (!kLateWeights) issue(0);
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
   int rpos = 0;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     if (SRC == SRC_NORM)
       inv = prod_norm_inv(prod_sumsq<SRC, 16, SPT>(pc, nchunk), K, pa.eps,
                           (double*)((char*)lds + w4a8_lds_bytes(K)));
-    if (kLateWeights) issue(0);
+    if (kLateWeights && SRC == SRC_NORM) issue(0);
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;
@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       const int4 q = prod_quant16(v, scale);
       w4a8_stage_put(q, scale, i, i < nchunk, nb, s_lo, s_hi, s_bs);
     }
+    if (kLateWeights && SRC != SRC_NORM) issue(0);
   } else if (!MULTI) {
     w4a8_stage_write<SPT>(st, s_lo, s_hi, s_bs, nchunk);
   } else {
