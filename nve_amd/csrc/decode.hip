@@ -166,8 +166,7 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
 // (OUT 3) the split's partial record (m, l, 0, 0, acc[D]).
 template <int D, int OUT, int SPLIT>
 __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&acc)[8], int hq, int sp, int num_heads,
-                                            int wave, int krow, int col, int tid, float* s_m, float* s_l, float* s_f,
-                                            float* s_ml, float* s_acc, uint16_t* __restrict__ out_bf16,
+                                            int wave, int krow, int col, int tid, float* s_m, float* s_l, float* s_acc, uint16_t* __restrict__ out_bf16,
                                             int8_t* __restrict__ out_q, float* __restrict__ out_s,
                                             float* __restrict__ out_part) {
   using T = AttnTile<D>;
@@ -184,29 +183,27 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
     }
   }
   lds_barrier();
-  // wave weights 2^(m_w - M) once (lanes 0..15 of wave 0), then every output column
-  // is a plain weighted sum of the 16 wave accumulators
-  if (tid < T::NW) {
+  // one barrier: every output lane reads the 16 wave maxima and sums, forms the wave
+  // weights 2^(m_w - M) itself (independent exp2, no second LDS round trip) and sums the
+  // 16 wave accumulators of its 4 columns
+  if (tid < D / 4) {
+    float mw[T::NW], lw[T::NW];
+#pragma unroll
+    for (int w = 0; w < T::NW; w += 4) {
+      const float4 m4 = *(const float4*)&s_m[w];
+      const float4 l4 = *(const float4*)&s_l[w];
+      mw[w] = m4.x, mw[w + 1] = m4.y, mw[w + 2] = m4.z, mw[w + 3] = m4.w;
+      lw[w] = l4.x, lw[w + 1] = l4.y, lw[w + 2] = l4.z, lw[w + 3] = l4.w;
+    }
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < T::NW; ++w) M = fmaxf(M, s_m[w]);
-    const float f = s_m[tid] == -INFINITY ? 0.0f : exp2f(s_m[tid] - M);
-    s_f[tid] = f;
-    if (tid == 0) {
-      float L = 0.0f;
-#pragma unroll
-      for (int w = 0; w < T::NW; ++w) L = fmaf(s_m[w] == -INFINITY ? 0.0f : exp2f(s_m[w] - M), s_l[w], L);
-      s_ml[0] = M;
-      s_ml[1] = L;
-    }
-  }
-  lds_barrier();
-  if (tid < D / 4) {
-    const float M = s_ml[0], L = s_ml[1];
+    for (int w = 0; w < T::NW; ++w) M = fmaxf(M, mw[w]);
+    float L = 0.0f;
     float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int w = 0; w < T::NW; ++w) {
-      const float f = s_f[w];
+      const float f = mw[w] == -INFINITY ? 0.0f : exp2f(mw[w] - M);
+      L = fmaf(f, lw[w], L);
       const float4 a4 = *(const float4*)&s_acc[w * D + 4 * tid];
       o[0] = fmaf(f, a4.x, o[0]);
       o[1] = fmaf(f, a4.y, o[1]);
@@ -253,7 +250,8 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   __shared__ float s_q[D];
   __shared__ __align__(16) uint16_t s_knew[D];
   __shared__ __align__(16) uint16_t s_vnew[D];
-  __shared__ float s_m[T::NW], s_l[T::NW], s_f[T::NW], s_ml[2];
+  __shared__ __align__(16) float s_m[T::NW];
+  __shared__ __align__(16) float s_l[T::NW];
   __shared__ __align__(16) float s_acc[T::NW * D];
 
   const int G = num_heads / num_kv_heads;
@@ -314,7 +312,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
                                acc);
       if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
     }
-    attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_f, s_ml, s_acc,
+    attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_acc,
                                out_bf16, out_q, out_s, out_part);
     return;
   }
@@ -370,7 +368,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
       attn_compute<D>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
     if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
   }
-  attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_f, s_ml, s_acc,
+  attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_acc,
                              out_bf16, out_q, out_s, out_part);
 }
 

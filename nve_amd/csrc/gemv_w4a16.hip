@@ -121,6 +121,15 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   // is staged (see gemv_w4a8.hip)
   constexpr bool kLateWeights = SRC == SRC_NORM || SRC == SRC_F32;
   if (!kLateWeights) issue(0);
+  // A late issue is fenced on both sides so that the loads leave as one group at that
+  // point: left to itself the scheduler spreads them through the quantization and hoists
+  // the unpacking of the first ones above the LDS stores, which then wait for HBM before
+  // the rest are even issued.
+  auto issue_pinned = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
   int rpos = 0;
   float rc[ROPE ? RH : 1], rs[ROPE ? RH : 1];
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
     if (SRC == SRC_NORM)
       inv = prod_norm_inv(prod_sumsq<SRC, 8, SPT>(pc, nchunk), K, pa.eps,
                           (double*)((char*)lds + w4a16_lds_bytes(MODE, K)));
-    if (kLateWeights && SRC == SRC_NORM) issue(0);
+    if (kLateWeights && SRC == SRC_NORM) issue_pinned();
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       prod_values<SRC, 8>(pc[s], inv, v);
       w4a16_stage_put_dot<MODE>(prod_bf16x8(v), i, i < nchunk, nb, s_p, s_mul);
     }
-    if (kLateWeights && SRC != SRC_NORM) issue(0);
+    if (kLateWeights && SRC != SRC_NORM) issue_pinned();
   } else if (!MULTI) {
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
@@ -172,6 +181,8 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
         w4a16_stage_put_dot<MODE>(x4[ic], i, i < nchunk, nb, s_p, s_mul);
     }
   }
+  // the weight arithmetic stays below the staging barrier
+  __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
 
   // (4) arithmetic

@@ -112,6 +112,15 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   // us).  The attention-merge producers keep the early issue (late was measured slower).
   constexpr bool kLateWeights = SRC == SRC_NORM || SRC == SRC_F32;
   if (!kLateWeights) issue(0);
+  // A late issue is fenced on both sides so that the loads leave as one group at that
+  // point: left to itself the scheduler spreads them through the quantization and hoists
+  // the unpacking of the first ones above the LDS stores, which then wait for HBM before
+  // the rest are even issued.
+  auto issue_pinned = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
   int rpos = 0;
   float rc[ROPE ? RH : 1], rs[ROPE ? RH : 1];
@@ -131,7 +140,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     if (SRC == SRC_NORM)
       inv = prod_norm_inv(prod_sumsq<SRC, 16, SPT>(pc, nchunk), K, pa.eps,
                           (double*)((char*)lds + w4a8_lds_bytes(K)));
-    if (kLateWeights && SRC == SRC_NORM) issue(0);
+    if (kLateWeights && SRC == SRC_NORM) issue_pinned();
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = (int)threadIdx.x + 256 * s;
@@ -141,12 +150,14 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       const int4 q = prod_quant16(v, scale);
       w4a8_stage_put(q, scale, i, i < nchunk, nb, s_lo, s_hi, s_bs);
     }
-    if (kLateWeights && SRC != SRC_NORM) issue(0);
+    if (kLateWeights && SRC != SRC_NORM) issue_pinned();
   } else if (!MULTI) {
     w4a8_stage_write<SPT>(st, s_lo, s_hi, s_bs, nchunk);
   } else {
     w4a8_stage_loop(xq, xs, s_lo, s_hi, s_bs, nchunk, pa.row_scale != nullptr);
   }
+  // the weight arithmetic stays below the staging barrier
+  __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
 
   float acc[R];
