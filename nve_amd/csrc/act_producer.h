@@ -107,10 +107,12 @@ __device__ __forceinline__ double prod_sumsq(const ProdChunk<SRC, E> (&c)[SPT], 
 }
 
 // 1 / sqrt(mean(h^2) + eps) over the K elements, reduced over the 256 threads of the
-// workgroup (wave butterflies, then 4 partials through LDS).  Every workgroup sums in
-// the same order, so all of them produce the same value.
+// workgroup (a DPP / permlane wave sum, then 4 partials through LDS).  Every workgroup
+// sums in the same order, so all of them produce the same value.  (The wave sum was six
+// __shfl_xor steps: twelve dependent ds_bpermute round trips, about 1 us of the
+// launch's critical path.)
 __device__ __forceinline__ double prod_norm_inv(double ss, int K, float eps, double* s_red) {
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  ss = group_sum_f64<64>(ss);
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
   lds_barrier();
   const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);

@@ -82,6 +82,44 @@ __device__ __forceinline__ float xor32_partner_max(float v) {
   return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
 }
 
+// f64 lane moves: the two halves travel separately through the same DPP / permlane
+// path.  Every step adds a lane's value to its partner's, and IEEE addition is
+// commutative, so both lanes of a pair (and in the end every lane) hold the same bits.
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+template <bool X32>
+__device__ __forceinline__ double xor_partner_sum_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+  const auto rl = X32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                      : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto rh = X32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                      : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  const double a = __builtin_bit_cast(double, ((uint64_t)(uint32_t)rh[0] << 32) | (uint32_t)rl[0]);
+  const double b = __builtin_bit_cast(double, ((uint64_t)(uint32_t)rh[1] << 32) | (uint32_t)rl[1]);
+  return a + b;
+}
+// f64 sum over aligned groups of N lanes, in every lane of the group (the order of
+// group_sum below).
+template <int N>
+__device__ __forceinline__ double group_sum_f64(double v) {
+  static_assert(N == 16 || N == 64, "group size");
+  v += dpp_mov_f64<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov_f64<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov_f64<0x141>(v);  // row_half_mirror
+  v += dpp_mov_f64<0x140>(v);  // row_mirror
+  if (N >= 64) {
+    v = xor_partner_sum_f64<false>(v);
+    v = xor_partner_sum_f64<true>(v);
+  }
+  return v;
+}
+
 // Sum over aligned groups of N lanes (N = 8, 16, 32 or 64), result in every lane of
 // the group: quad butterflies, then the half-row and row mirrors (a mirror maps one
 // half of the group onto the other), then the permlane swaps.

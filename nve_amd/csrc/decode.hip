@@ -37,12 +37,12 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
     const double v = (double)h[i];
     ss += v * v;
   }
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  ss = group_sum_f64<64>(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   if (threadIdx.x < 64) {
     double v = threadIdx.x < 16 ? red[threadIdx.x] : 0.0;
-    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    v = group_sum_f64<16>(v);
     if (threadIdx.x == 0) red[0] = v;
   }
   __syncthreads();

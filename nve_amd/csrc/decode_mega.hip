@@ -203,8 +203,7 @@ __device__ __forceinline__ double stage_sumsq(const ProdChunk<SRC, E> (&pc)[SPT]
       ss += ok ? q : 0.0;
     }
   }
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-  return ss;
+  return group_sum_f64<64>(ss);
 }
 
 template <bool W4A8>
