@@ -413,8 +413,31 @@ __device__ __forceinline__ void argmax_merge(float& b, int& bi, float o, int oi)
   }
 }
 
+// Wave butterfly on DPP / permlane moves (the steps of group_sum): the merge is
+// symmetric (larger value, or the lower index of equal values), so both lanes of a pair
+// keep the same (value, index) and every lane ends with the wave's result.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& b, int& bi) {
+  argmax_merge(b, bi, dpp_mov<CTRL>(b), dpp_mov_i<CTRL>(bi));
+}
+template <bool X32>
+__device__ __forceinline__ void argmax_xor(float& b, int& bi) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, b), ui = (uint32_t)bi;
+  const auto r = X32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false) : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const auto ri = X32 ? __builtin_amdgcn_permlane32_swap(ui, ui, false, false)
+                      : __builtin_amdgcn_permlane16_swap(ui, ui, false, false);
+  // one of the two results is the lane's own pair (a no-op merge), the other its partner's
+  argmax_merge(b, bi, __builtin_bit_cast(float, (uint32_t)r[0]), (int)ri[0]);
+  argmax_merge(b, bi, __builtin_bit_cast(float, (uint32_t)r[1]), (int)ri[1]);
+}
+
 __device__ __forceinline__ void argmax_block(float& best, int& bi, float* s_v, int* s_i) {
-  for (int off = 32; off > 0; off >>= 1) argmax_merge(best, bi, __shfl_xor(best, off, 64), __shfl_xor(bi, off, 64));
+  argmax_dpp<0xB1>(best, bi);   // quad_perm [1,0,3,2]
+  argmax_dpp<0x4E>(best, bi);   // quad_perm [2,3,0,1]
+  argmax_dpp<0x141>(best, bi);  // row_half_mirror
+  argmax_dpp<0x140>(best, bi);  // row_mirror
+  argmax_xor<false>(best, bi);
+  argmax_xor<true>(best, bi);
   if ((threadIdx.x & 63) == 0) {
     s_v[threadIdx.x >> 6] = best;
     s_i[threadIdx.x >> 6] = bi;

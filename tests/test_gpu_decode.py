@@ -315,3 +315,50 @@ def test_decode_mega_matches_five_launch_layer(torch_dev, shape, monkeypatch):
         pos = m.prefill
         ka, kb = mega1[1][:, pos].float(), five[1][:, pos].float()
         assert torch.allclose(ka, kb, rtol=2.0 ** -7, atol=TOL_LAYER * float(kb.pow(2).mean().sqrt()))
+
+
+@pytest.mark.parametrize("lm8", [True, False])
+def test_head_argmax_ties_nan_and_slices(torch_dev, lm8):
+    """Greedy argmax of the head across all 128 partial workgroups (vocab 200000: every
+    slice holds logits): among equal logits the lowest index wins, NaN never wins
+    (src/ops.rs:485-495 keeps the first maximum), including ties that span slices."""
+    torch = torch_dev
+    vocab = 200_000
+    m = _model(torch, 4, 2, 64, layers=1, vocab=vocab, lm_head_w4a8=lm8, prefill=4, max_seq=16)
+    nib, sc = m.lm_head
+    nb = sc.numel() // vocab
+    sc0, nib0 = sc.clone(), nib.clone()
+
+    def run():
+        m.start(3)
+        m.head()
+        torch.cuda.synchronize()
+        return int(m.token.item()), m.logits.cpu().numpy()
+
+    # every logit 0: the first index
+    sc.zero_()
+    tok, lg = run()
+    assert np.all(lg == 0.0) and tok == 0
+    # NaN rows in front of the zeros: the first non-NaN row
+    for k in (1, 5000, 150_001):
+        sc.zero_()
+        sc.view(vocab, nb)[:k] = float("nan")
+        tok, lg = run()
+        assert np.isnan(lg[:k]).all() and tok == k, (k, tok)
+    # one row copied to later slices, everything else 0: the first maximum
+    r0, copies = 70_000, (70_001, 140_000, 199_999)
+    sc.zero_()
+    sc.view(vocab, nb)[r0] = sc0.view(vocab, nb)[r0]
+    rb = nib.numel() // vocab
+    for r in copies:
+        sc.view(vocab, nb)[r] = sc0.view(vocab, nb)[r0]
+        nib.view(vocab, rb)[r] = nib0.view(vocab, rb)[r0]
+    nib.view(vocab, rb)[r0] = nib0.view(vocab, rb)[r0]
+    tok, lg = run()
+    assert lg[r0] != 0.0 and all(lg[r] == lg[r0] for r in copies)
+    expect = r0 if lg[r0] > 0 else 0
+    assert tok == expect, (tok, expect, lg[r0])
+    # a NaN among the copies changes nothing for the others
+    sc.view(vocab, nb)[r0] = float("nan")
+    tok, lg = run()
+    assert tok == (copies[0] if lg[copies[0]] > 0 else 0), tok
