@@ -5,13 +5,15 @@
 // or the per-row bf16 scale (per-token mode, applied once per row: the sum over
 // blocks is formed with ws only and multiplied by the row scale at the end).
 //
-// M = 1 runs the one-shot W4A8 GEMV (gemv_w4a8.hip).
+// M = 1 runs the one-shot W4A8 GEMV (gemv_w4a8.hip), M = 2 the staged v_dot4 kernel
+// below (where its LDS fits), larger M the int8 MFMA kernel.
 // v_dot4 kernel (any M >= 2 under NVE_GEMV_ONESHOT): one wave per output row, lane l owns
 // blocks l, l+64, ...; the nibbles are turned into signed int8 (nib - 8) once per
 // block with (t + 0x78787878) ^ 0x80808080 (no carries cross bytes for t <= 15), and
 // every activation row reuses them through 8 v_dot4_i32_i8.
 #include "common.h"
 #include "w4_launch.h"
+#include "w4a8_ops.h"
 
 namespace nve {
 
@@ -74,6 +76,142 @@ __global__ __launch_bounds__(256) void w4a8_batched_dot4_kernel(int M, const int
       float v = wave_sum_to_lane63(acc[m]);
       if (XS_MODE == NVE_XS_ROW_BF16) v *= bf16_bits_to_f32(((const uint16_t*)xs)[m]);
       if (lane == 63 && row < N) store_out<OUT_DT>(out, (size_t)m * N + row, v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Staged v_dot4 kernel (small M): the one-row GEMV's structure (gemv_w4a8.hip) with
+// the M activation rows staged in LDS, each in the one-row kernel's planes (lo / hi
+// halves of every block, {sum(xq), bits(xs)}).  A wave owns R weight rows, lane l owns
+// blocks l, l + 64, ...; every weight load is issued before any arithmetic; a block's
+// nibbles are masked once and meet each activation row through 8 v_dot4 (the block
+// order per lane and the fma per block are the one-row kernel's, so the per-row result
+// is the same arithmetic as M one-row launches).  Per-token mode stages unit block
+// scales and multiplies each row sum by the row's bf16 scale.
+__host__ __device__ constexpr int staged_row_int4(int K) {  // LDS int4 units per activation row
+  return 2 * (K / 32 + 1) + (K / 32 + 2) / 2;
+}
+
+template <int OUT_DT, int XS_MODE, int MM, int R, int NJ>
+__global__ __launch_bounds__(256) void w4a8_batched_staged_kernel(int M, const int8_t* __restrict__ xq,
+                                                                  const void* __restrict__ xs,
+                                                                  const uint8_t* __restrict__ nib,
+                                                                  const float* __restrict__ ws,
+                                                                  void* __restrict__ out, int N, int K) {
+  constexpr int SPT = (NJ + 1) / 2;  // staging passes per row: 2*nb <= 128*NJ chunks of 16 B
+  extern __shared__ int4 lds[];
+  const int nb = K >> 5;
+  const int nchunk = 2 * nb;
+  const int rs = staged_row_int4(K);
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+
+  // (1) staging loads of every activation row (clamped index, unconditional)
+  int4 sv[MM][SPT];
+  float sx[MM][SPT];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const int mc = min(m, M - 1);
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = min((int)threadIdx.x + 256 * s, nchunk - 1);
+      sv[m][s] = ((const int4*)(xq + (size_t)mc * K))[i];
+      sx[m][s] = XS_MODE == NVE_XS_GROUP32_F32 ? ((const float*)xs)[(size_t)mc * nb + (i >> 1)] : 1.0f;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // (2) weight loads (blocks past the end of a row re-load block nb-1, zeroed at use)
+  uint4 wv[R][NJ];
+  float wsc[R][NJ];
+  const size_t row_bytes = (size_t)(K >> 1);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, N - 1);
+    const uint4* rn = (const uint4*)(nib + (size_t)row * row_bytes);
+    const float* rsc = ws + (size_t)row * nb;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int bb = min(lane + 64 * j, nb - 1);
+      wv[r][j] = ld_stream(rn + bb);
+      wsc[r][j] = ld_stream(rsc + bb);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // (3) LDS writes (wait only for the older staging loads)
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    if (m < M) {
+      int4* base = lds + (size_t)m * rs;
+#pragma unroll
+      for (int s = 0; s < SPT; ++s) {
+        const int i = (int)threadIdx.x + 256 * s;
+        w4a8_stage_put(sv[m][s], sx[m][s], i, i < nchunk, nb, base, base + (nb + 1), (int2*)(base + 2 * (nb + 1)));
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+
+  // (4) arithmetic
+  float acc[R][MM];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = 0.0f;
+  const unsigned MASK = 0x0F0F0F0Fu;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int b = lane + 64 * j;
+    const int bb = min(b, nb - 1);
+    int4 lo[MM], hi[MM];
+    int sq[MM];
+    float xsf[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      if (m < M) {
+        const int4* base = lds + (size_t)m * rs;
+        lo[m] = base[bb];
+        hi[m] = base[(nb + 1) + bb];
+        const int2 bs = ((const int2*)(base + 2 * (nb + 1)))[bb];
+        sq[m] = bs.x;
+        xsf[m] = b < nb ? __builtin_bit_cast(float, bs.y) : 0.0f;  // lanes past the end add nothing
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint4 w = wv[r][j];
+      const int w0 = (int)(w.x & MASK), w1 = (int)((w.x >> 4) & MASK), w2 = (int)(w.y & MASK),
+                w3 = (int)((w.y >> 4) & MASK), w4 = (int)(w.z & MASK), w5 = (int)((w.z >> 4) & MASK),
+                w6 = (int)(w.w & MASK), w7 = (int)((w.w >> 4) & MASK);
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        if (m < M) {
+          int d = 0;
+          d = __builtin_amdgcn_sdot4(w0, lo[m].x, d, false);
+          d = __builtin_amdgcn_sdot4(w1, hi[m].x, d, false);
+          d = __builtin_amdgcn_sdot4(w2, lo[m].y, d, false);
+          d = __builtin_amdgcn_sdot4(w3, hi[m].y, d, false);
+          d = __builtin_amdgcn_sdot4(w4, lo[m].z, d, false);
+          d = __builtin_amdgcn_sdot4(w5, hi[m].z, d, false);
+          d = __builtin_amdgcn_sdot4(w6, lo[m].w, d, false);
+          d = __builtin_amdgcn_sdot4(w7, hi[m].w, d, false);
+          acc[r][m] = fmaf(wsc[r][j] * xsf[m], (float)(d - 8 * sq[m]), acc[r][m]);
+        }
+      }
+    }
+  }
+  // (5) row sums
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    if (m < M) {
+      const float rsc = XS_MODE == NVE_XS_ROW_BF16 ? bf16_bits_to_f32(((const uint16_t*)xs)[m]) : 1.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float v = wave_sum_to_lane63(acc[r][m]);
+        if (XS_MODE == NVE_XS_ROW_BF16) v *= rsc;
+        if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)m * N + row0 + r, v);
+      }
     }
   }
 }
@@ -285,6 +423,47 @@ static hipError_t launch_mfma_m(int M, const int8_t* xq, const void* xs, const u
   return launch_mfma<OUT_DT, XS, 4>(M, xq, xs, nib, ws, out, N, K, stream);
 }
 
+// Staged v_dot4 kernel: the one-row GEMV's tiling (R rows per wave, NJ 64-block chunks
+// per lane, one staging pass), the activation rows in LDS.  It serves M = 2 where the
+// two staged rows take at most 40 KB of LDS (8B gate 14336x4096: 9.2 us against 11.3 us
+// on MFMA; down 4096x14336: 10.4 against 10.5).  From M = 3 the per-workgroup staging
+// (every workgroup stages every row) and the M-fold LDS operand reads cost more than the
+// MFMA kernel's transposes (gate M = 4: 12.1 against 11.6 us).
+static constexpr int kStagedM = 2;
+static size_t staged_lds_bytes(int M, int K) { return (size_t)M * nve::staged_row_int4(K) * 16; }
+
+static bool staged_fits(int M, int N, int K) {
+  if (M != kStagedM) return false;
+  W4Segs s{};
+  s.nseg = 1;
+  s.n[0] = N;
+  return !choose_w4_tiling(s, K).multi && staged_lds_bytes(M, K) <= 40 * 1024;
+}
+
+template <int OUT_DT, int XS>
+static hipError_t launch_staged(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
+                                void* out, int N, int K, hipStream_t stream) {
+  W4Segs s{};
+  s.nseg = 1;
+  s.n[0] = N;
+  const W4Tiling t = choose_w4_tiling(s, K);
+  const size_t lds = staged_lds_bytes(M, K);
+  const int grid = (N + 4 * t.R - 1) / (4 * t.R);
+#define NVE_STAGED_CASE(RR, JJ, MM)                                                                          \
+  if (!MM && t.R == RR && t.NJ == JJ) {                                                                      \
+    auto kern = nve::w4a8_batched_staged_kernel<OUT_DT, XS, kStagedM, RR, JJ>;                           \
+    if (lds > 65536) {                                                                                       \
+      hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+      if (e != hipSuccess) return e;                                                                         \
+    }                                                                                                        \
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, M, xq, xs, nib, ws, out, N, K);             \
+    return hipGetLastError();                                                                                \
+  }
+  NVE_W4_TILING_CASES(NVE_STAGED_CASE)
+#undef NVE_STAGED_CASE
+  return hipErrorInvalidValue;
+}
+
 template <int OUT_DT>
 static hipError_t launch_batched_o(int M, const int8_t* xq, const void* xs, int xs_mode,
                                    const uint8_t* nib, const float* ws, void* out, int N, int K,
@@ -300,6 +479,11 @@ static hipError_t launch_batched_o(int M, const int8_t* xq, const void* xs, int 
     s.n[0] = N;
     if (xs_mode == NVE_XS_ROW_BF16) return launch_w4a8_rowscale(xq, (const uint16_t*)xs, s, OUT_DT, K, stream);
     return launch_w4a8(xq, (const float*)xs, s, OUT_DT, K, stream);
+  }
+  if (staged_fits(M, N, K)) {
+    if (xs_mode == NVE_XS_ROW_BF16)
+      return launch_staged<OUT_DT, NVE_XS_ROW_BF16>(M, xq, xs, nib, ws, out, N, K, stream);
+    return launch_staged<OUT_DT, NVE_XS_GROUP32_F32>(M, xq, xs, nib, ws, out, N, K, stream);
   }
   if (batched_use_mfma()) {
     if (xs_mode == NVE_XS_ROW_BF16)

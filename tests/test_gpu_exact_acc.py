@@ -207,9 +207,10 @@ def test_w4a8_grouped_exact(orc, env, ns, k, mode):
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("xs_mode", ["group_f32", "row_bf16"])
 def test_w4a8_batched_exact(orc, env, n, k, m, xs_mode):
-    """Batched W4A8: M = 1 on v_dot4, M >= 2 on int8 MFMA (with the -8 correction
-    MFMA); every row of every activation exact.  Row mode: one power-of-two bf16 scale
-    per activation row (bf16 2^e is exact)."""
+    """Batched W4A8: M = 1 on the one-row GEMV, M = 2 on the staged v_dot4 kernel (the
+    shapes here all fit its LDS), M >= 3 on int8 MFMA (with the -8 correction MFMA);
+    every row of every activation exact.  Row mode: one power-of-two bf16 scale per
+    activation row (bf16 2^e is exact)."""
     torch, hk, L, pol = env
     print(f"exact batched n={n} k={k} m={m} xs={xs_mode}", flush=True)
     nib, ws = _weights(n, k, seed=n + k + m, ws_spread=_spread(k))
@@ -225,6 +226,33 @@ def test_w4a8_batched_exact(orc, env, n, k, m, xs_mode):
         ts = _up(torch, xs)
     y = hk.matvec_w4a8_batched(tq, ts, _up(torch, nib), _up(torch, ws), n, k, out_dtype=torch.float32)
     torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    bad = got.view(np.uint32) != refs.view(np.uint32)
+    assert not bad.any(), f"{int(bad.sum())} of {bad.size} outputs differ"
+
+
+@pytest.mark.parametrize("n,k", [(300, 2048), (4096, 14336)])
+@pytest.mark.parametrize("m", [3, 5])
+@pytest.mark.parametrize("xs_mode", ["group_f32", "row_bf16"])
+def test_w4a8_batched_dot4_exact(orc, env, n, k, m, xs_mode):
+    """The v_dot4 batched kernel (one wave per row, activations read per row), which the
+    one-shot kernel policy selects for M >= 3: exact like the other batched kernels."""
+    torch, hk, L, pol = env
+    print(f"exact batched dot4 n={n} k={k} m={m} xs={xs_mode}", flush=True)
+    nib, ws = _weights(n, k, seed=n + k + m + 1, ws_spread=_spread(k))
+    xq, e = _acts(k, seed=k + 19 * m, m=m)
+    if xs_mode == "row_bf16":
+        e = np.repeat(e[:, :1], k // 32, axis=1)
+    xs = np.ldexp(np.float32(1.0), e).astype(np.float32)
+    refs = np.stack([_expected(orc, xq[i], xs[i], nib, ws, n, k) for i in range(m)])
+    tq = _up(torch, xq)
+    ts = _up(torch, xs[:, 0].copy()).to(torch.bfloat16) if xs_mode == "row_bf16" else _up(torch, xs)
+    L.nve_hip_set_gemv_policy(pol["oneshot"], 2, 4)
+    try:
+        y = hk.matvec_w4a8_batched(tq, ts, _up(torch, nib), _up(torch, ws), n, k, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        L.nve_hip_set_gemv_policy(pol["auto"], 2, 4)
     got = y.cpu().numpy()
     bad = got.view(np.uint32) != refs.view(np.uint32)
     assert not bad.any(), f"{int(bad.sum())} of {bad.size} outputs differ"
