@@ -333,6 +333,28 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40, suite=SU
                                        "gemv_per_s": round(1e6 / us), "bytes": b,
                                        "GBs": round(b / us / 1e3, 1), "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
             log(f"  {label:15s} {prec:6s} {us:8.2f} us {b / us / 1e3:8.1f} GB/s {100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}%")
+    # the reference's own W4A16 entry point: nve_matvec_w4a16 (fp16 in, fp16 out, no AWQ)
+    for name, n, k in suite:
+        if name not in ("gate_proj", "down_proj", "lm_head"):
+            continue
+        sets = weights[name]
+        x16 = acts["h16"] if k == hid else acts["mid16"]
+        out = torch.empty(n, dtype=torch.float16, device="cuda")
+
+        def body(sets=sets, x16=x16, out=out, n=n, k=k):
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(launches_per_graph):
+                nib, sc = sets[i % len(sets)]
+                L.nve_matvec_w4a16(x16.data_ptr(), nib.data_ptr(), sc.data_ptr(), None, out.data_ptr(), n, k, s)
+        body()
+        g = capture(torch, body)
+        time_graphs(torch, [g], 2)
+        us = time_graphs(torch, [g], 3 if name == "lm_head" else 10) * 1e3 / launches_per_graph
+        b = gemv_bytes(n, k, "w4a16", 2)
+        rows[f"{name}/w4a16_f16_dropin"] = {"N": n, "K": k, "us": round(us, 3), "gemv_per_s": round(1e6 / us),
+                                             "bytes": b, "GBs": round(b / us / 1e3, 1),
+                                             "frac_peak": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"  {name:10s} w4a16 fp16 drop-in {us:8.2f} us {b / us / 1e3:8.1f} GB/s")
     return rows
 
 
