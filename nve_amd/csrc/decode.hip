@@ -84,10 +84,14 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 // The new token's key is rotated and rounded to bf16 like every cached entry; the
 // workgroup of the kv head's first query head writes it and the value to the cache,
 // the others use their own identical copy for that row.
+// One key slot per lane per tile (64-key tiles at D = 128): against two slots (128-key
+// tiles) the 3B decode runs 1081 against 1064 tok/s at 512 cached keys and 826 against
+// 820 at 7000 -- a workgroup streams its K/V through one CU, and the smaller tile
+// shortens that stream's first wait and its tail.
 template <int D>
 struct AttnTile {
   static constexpr int NW = 16;         // waves per workgroup
-  static constexpr int P = 2;           // key slots per lane per tile
+  static constexpr int P = 1;           // key slots per lane per tile
   static constexpr int LPK = D / 8;     // lanes per key
   static constexpr int KPW = 64 / LPK;  // keys per wave per slot
   static constexpr int KT = NW * KPW * P;
@@ -678,9 +682,9 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
 }
 
 // Key splits of the fused decode attention (the partials are merged in the o_proj
-// GEMV's staging), chosen from the cache capacity: one workgroup streams about
-// 60 GB/s and computes one 128-key tile per head in about 1.3 us, so caches past a
-// few hundred keys need more workgroups per head; the merging o_proj launch uses few
+// GEMV's staging), chosen from the cache capacity: a workgroup's K/V stream passes
+// through one CU (about 60 GB/s), so caches past a few hundred keys need more
+// workgroups per head; the merging o_proj launch uses few
 // workgroups, so the merge costs little.  Eight splits hold 8 partial chunks in the
 // o_proj staging registers, which fits one staging pass (num_heads * head_dim <= 4096);
 // wider layers use four.  NVE_ATTN_SPLIT=1/2/4/8 overrides (8 only where it fits).
