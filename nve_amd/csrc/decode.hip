@@ -299,23 +299,44 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     const int len = pos + 1;
     const int ntiles = (len + T::KT - 1) / T::KT;
     const int nt = ntiles > sp ? (ntiles - sp + SPLIT - 1) / SPLIT : 0;
-    if (nt > 1) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, len, wave, krow, col);
-    if (nt > 2) attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, len, wave, krow, col);
+    // The ring's loads are issued unconditionally wherever they precede the steady-state
+    // loop (rows past the length clamp to the last live row: a tile the split does not
+    // have costs one cached row per load), so the waits inside the loop count the two
+    // younger tiles' loads exactly: with conditional issues the compiler drained the
+    // whole ring (vmcnt(0)) before every third tile.
+    attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT, len, wave, krow, col);
+    attn_issue<D>(b2, kc, vc, cache_base, sp + 2 * SPLIT, len, wave, krow, col);
     float m_run = -INFINITY, l_run = 0.0f, acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int j = 0; j < nt; j += 3) {
+    int j = 0;
+    for (; j + 5 < nt; j += 3) {  // every refill is a live tile
       attn_compute<D, false>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
-      if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
-      if (j + 1 < nt)
-        attn_compute<D, false>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
-                               acc);
-      if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
-      if (j + 2 < nt)
-        attn_compute<D, false>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
-                               acc);
-      if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
+      attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
+      attn_compute<D, false>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                             acc);
+      attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
+      attn_compute<D, false>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                             acc);
+      attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
     }
+    // the last five tiles at most: b0, b1, b2 hold tiles j, j + 1, j + 2
+    if (j < nt)
+      attn_compute<D, false>(b0, sp + SPLIT * j, len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run, acc);
+    if (j + 3 < nt) attn_issue<D>(b0, kc, vc, cache_base, sp + SPLIT * (j + 3), len, wave, krow, col);
+    if (j + 1 < nt)
+      attn_compute<D, false>(b1, sp + SPLIT * (j + 1), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                             acc);
+    if (j + 4 < nt) attn_issue<D>(b1, kc, vc, cache_base, sp + SPLIT * (j + 4), len, wave, krow, col);
+    if (j + 2 < nt)
+      attn_compute<D, false>(b2, sp + SPLIT * (j + 2), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                             acc);
+    if (j + 3 < nt)
+      attn_compute<D, false>(b0, sp + SPLIT * (j + 3), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                             acc);
+    if (j + 4 < nt)
+      attn_compute<D, false>(b1, sp + SPLIT * (j + 4), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
+                             acc);
     attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_acc,
                                out_bf16, out_q, out_s, out_part);
     return;
