@@ -400,17 +400,24 @@ namespace nve_host {
 // the kernel-selection policy forces one-shot v_dot4 kernels (nve_hip_set_gemv_policy(NVE_GEMV_ONESHOT, ...)).
 static bool batched_use_mfma() { return gemv_policy() != NVE_GEMV_ONESHOT; }
 
-// 16 waves per workgroup (the K quads are dealt round-robin); two 16-row tiles per
-// workgroup while that still leaves at least 256 workgroups, else one.
+// 16 waves per workgroup (the K quads are dealt round-robin) and 1, 2 or 4 16-row tiles
+// per workgroup: the fewest that keep the grid within one workgroup per CU (one
+// 1024-thread workgroup fits a CU), since a second round of workgroups starts only as
+// the first drains (8B gate, 14336 rows: 224 workgroups of 4 tiles take 10.9 / 11.2 /
+// 11.8 us at M = 4 / 8 / 16 against 11.6 / 12.1 / 13.2 for 448 of 2).
 template <int OUT_DT, int XS, int EU>
 static hipError_t launch_mfma(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
                               void* out, int N, int K, hipStream_t stream) {
   const int vec_sc = (K % 128 == 0) && aligned(ws, 16);
-  if ((N + 31) / 32 >= 256)
+  constexpr int kCU = 256;
+  if ((N + 15) / 16 <= kCU)
+    hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, 16, 1, EU>), dim3((N + 15) / 16), dim3(1024), 0,
+                       stream, M, xq, xs, nib, ws, out, N, K, vec_sc);
+  else if ((N + 31) / 32 <= kCU)
     hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, 16, 2, EU>), dim3((N + 31) / 32), dim3(1024), 0,
                        stream, M, xq, xs, nib, ws, out, N, K, vec_sc);
   else
-    hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, 16, 1, EU>), dim3((N + 15) / 16), dim3(1024), 0,
+    hipLaunchKernelGGL((nve::w4a8_batched_mfma_kernel<OUT_DT, XS, 16, 4, EU>), dim3((N + 63) / 64), dim3(1024), 0,
                        stream, M, xq, xs, nib, ws, out, N, K, vec_sc);
   return hipGetLastError();
 }
