@@ -157,8 +157,9 @@ int nve_hip_grouped_matvec_w4a8_x(const void *x, int x_dtype, const nve_w4_mat *
 /* Batched W4A8 (small-batch decode, 1 <= M <= NVE_MAX_M).  xq [M,K]; xs_mode
  * NVE_XS_GROUP32_F32: xq_scales f32 [M, K/32]; NVE_XS_ROW_BF16: bf16 [M].
  * out [M, N] of out_dtype.  M = 1 runs on the one-shot W4A8 GEMV (per-token mode: unit
- * block scales, the row scale applied to the row sums), M = 2 on a v_dot4 kernel with
- * both rows staged in LDS (where they fit in 40 KB), larger M on int8 MFMA. */
+ * block scales, the row scale applied to the row sums), M >= 2 on int8 MFMA (K % 128 == 0
+ * and N <= 16384: the LDS-ring kernel; otherwise a register kernel, and for M = 2 a
+ * v_dot4 kernel with both rows staged in LDS where they fit in 40 KB). */
 int nve_hip_matvec_w4a8_batched(int M, const int8_t *xq, const void *xq_scales, int xs_mode,
                                 const uint8_t *nibbles, const float *wt_scales, void *out,
                                 int out_dtype, int N, int K, void *stream);

@@ -5,8 +5,9 @@
 // or the per-row bf16 scale (per-token mode, applied once per row: the sum over
 // blocks is formed with ws only and multiplied by the row scale at the end).
 //
-// M = 1 runs the one-shot W4A8 GEMV (gemv_w4a8.hip), M = 2 the staged v_dot4 kernel
-// below (where its LDS fits), larger M the int8 MFMA kernel.
+// M = 1 runs the one-shot W4A8 GEMV (gemv_w4a8.hip); M >= 2 the LDS-ring int8 MFMA
+// kernel where K % 128 == 0 and N <= 16384, otherwise the staged v_dot4 kernel for M = 2
+// (where its LDS fits) and the register int8 MFMA kernel.
 // v_dot4 kernel (any M >= 2 under NVE_GEMV_ONESHOT): one wave per output row, lane l owns
 // blocks l, l+64, ...; the nibbles are turned into signed int8 (nib - 8) once per
 // block with (t + 0x78787878) ^ 0x80808080 (no carries cross bytes for t <= 15), and
@@ -392,6 +393,267 @@ __global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_kernel(int M, const
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// LDS-ring int8 MFMA kernel (M >= 3, K % 128 == 0, N <= 256 * 64).
+//
+// Same operand mapping as the kernel above; what changes is how the bytes reach the
+// operand lanes.  The register kernel moves every loaded dword to its operand lane
+// with ds_bpermute and holds its loads in VGPRs, and its per-quad instruction count
+// (about 200 per wave and quad at one tile) makes it issue-bound.  Here every load is
+// a global -> LDS transfer (global_load_lds, no VGPRs in flight) into a per-wave ring
+// of S slots, each holding one K quad:
+//   W  T x 1 KiB   weight tile t, the row-major load layout (16 rows x 64 B, 4 lanes per row)
+//   SC T x 256 B   the tile's 16 x 4 block scales (row-major)
+//   A  MA x 1 KiB  activation rows 8a..8a+7, 128 B each (blocks 4q..4q+3)
+//   XS 256 B       (group-scale mode) the quad's 4 scales of each activation row
+// and the operand lanes read the slot directly: the tile's dword g of the 4 blocks is
+// one ds_read_b128 (piece g of row n) and the 4x4 permlane transpose; the activation
+// operand (dword g of both halves of each block) four ds_read2_b32; the scales one
+// ds_read_b128.  A transfer writes its lanes' 16 bytes contiguously, so rows sit 64 B
+// (weights) or 128 B (activations) apart and a column read would hit one bank group
+// (8-way and 16-way conflicts on the CU's shared LDS, which bound the kernel); the
+// sources are swizzled instead -- load lane (row a, slot s) fetches weight piece
+// (s - a / 2) & 3, activation row m's blocks are rotated by m % 4 -- so each transfer
+// still covers whole rows (coalesced) and the operand reads are conflict-free.  The issue is unconditional (quads past the wave's share are clamped
+// to the last quad) so every quad is the same number of loads and the waits are exact
+// vmcnt immediates: S quads in flight through the steady loop, an unrolled drain.
+// Workgroups take ceil(N / 256) consecutive rows each (T = ceil(rows / 16) tiles, the
+// last one partly masked), so the grid is at most one workgroup per CU and every CU
+// streams the same number of weight bytes; masked lanes issue no loads.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void lds_dma16(const void* g, char* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)l, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* g, char* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)l, 4, 0, 0);
+}
+
+// Ring reads are inline asm: the compiler's wait insertion cannot tell the ring slots
+// apart and would drain every transfer in flight (vmcnt(0)) before each LDS read of a
+// slot that a transfer has targeted.  The slot's own transfers are waited for with the
+// exact vmcnt above; the reads' results are waited for with lgkm_wait() and passed
+// through tie() so no use is scheduled above that wait.
+typedef __attribute__((address_space(3))) const char lds_cchar_t;
+__device__ __forceinline__ uint32_t lds_addr(const char* p) { return (uint32_t)(uintptr_t)(lds_cchar_t*)p; }
+__device__ __forceinline__ u32x4_t ds_read128(uint32_t a) {
+  u32x4_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+template <int O0, int O1>
+__device__ __forceinline__ u32x2_t ds_read2(uint32_t a) {
+  u32x2_t v;
+  asm volatile("ds_read2_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(v) : "v"(a), "i"(O0), "i"(O1));
+  return v;
+}
+__device__ __forceinline__ void lgkm_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <class V>
+__device__ __forceinline__ void tie(V& v) {
+  asm volatile("" : "+v"(v));
+}
+
+template <int T, int EU, int XS_MODE>
+struct RingLayout {
+  static constexpr int MA = EU == 4 ? 2 : 1;  // activation transfers per quad
+  static constexpr int XG = XS_MODE == NVE_XS_GROUP32_F32 ? 1 : 0;
+  static constexpr int W = 0, SC = T * 1024, A = SC + T * 256, XS = A + MA * 1024;
+  static constexpr int SLOT = XS + XG * 256;
+  static constexpr int LOADS = 2 * T + MA + XG;  // vmcnt events per quad
+};
+
+template <int OUT_DT, int XS_MODE, int KS, int T, int EU, int S>
+__global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_lds_kernel(int M, const int8_t* __restrict__ xq,
+                                                                        const void* __restrict__ xs,
+                                                                        const uint8_t* __restrict__ nib,
+                                                                        const float* __restrict__ ws,
+                                                                        void* __restrict__ out, int N, int K,
+                                                                        int rows_per_wg) {
+  static_assert(S >= 1 && S <= 4, "ring depth");
+  using L = RingLayout<T, EU, XS_MODE>;
+  constexpr int kRing = KS * S * L::SLOT;
+  constexpr int kRed = KS * T * 16 * (4 * EU + 1) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kRing > kRed ? kRing : kRed];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nl = lane & 15, g = lane >> 4;  // operand layout
+  const int lr = lane >> 2, lp = lane & 3;  // load layout
+  const int row0 = blockIdx.x * rows_per_wg;
+  const int nb = K >> 5, nq = nb >> 2;
+  const int nqw = (nq + KS - 1) / KS;  // quads per wave (the host guarantees nqw >= S)
+  char* const ring = smem + wave * (S * L::SLOT);
+
+  // per-lane sources at quad 0 (advanced by the quad index at issue)
+  const uint8_t* wsrc[T];
+  const float* ssrc[T];
+  bool wok[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int rr = 16 * t + lr;
+    const int r = min(row0 + rr, N - 1);
+    wok[t] = (rr < rows_per_wg && row0 + rr < N) || lane == 0;  // lane 0 keeps every transfer issued
+    wsrc[t] = nib + (size_t)r * (K >> 1) + 16 * ((lp - (lr >> 1)) & 3);  // swizzled piece
+    ssrc[t] = ws + (size_t)r * nb + lp;
+  }
+  const int8_t* asrc[L::MA];
+  bool aok[L::MA];
+#pragma unroll
+  for (int a = 0; a < L::MA; ++a) {
+    const int m = 8 * a + (lane >> 3);
+    aok[a] = m < M;
+    asrc[a] = xq + (size_t)min(m, M - 1) * K + 16 * (((lane & 7) - 2 * (lane >> 3)) & 7);  // rotated blocks
+  }
+  const float* xsrc = (const float*)xs + (size_t)min(lr, M - 1) * nb + lp;
+  const bool xok = lr < M;
+
+  auto issue = [&](int i) {
+    const int q = min(wave + KS * i, nq - 1);
+    char* const sb = ring + (i % S) * L::SLOT;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (wok[t]) lds_dma16(wsrc[t] + 64 * q, sb + L::W + t * 1024);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (wok[t]) lds_dma4(ssrc[t] + 4 * q, sb + L::SC + t * 256);
+#pragma unroll
+    for (int a = 0; a < L::MA; ++a)
+      if (aok[a]) lds_dma16(asrc[a] + 128 * q, sb + L::A + a * 1024);
+    if (L::XG && xok) lds_dma4(xsrc + 4 * q, sb + L::XS);
+  };
+
+  const int am = 4 * (nl & 3) + (nl >> 2);  // activation row of A row nl
+  // slot offsets read by this lane (see the swizzles above): weight piece g of row nl,
+  // and the lo / hi halves of block j of activation row am (rows >= M read row M - 1)
+  const uint32_t rd_w = 16 * (4 * nl + ((g + (nl >> 1)) & 3));
+  uint32_t rd_a[4];
+  {
+    const int ar = min(am, M - 1);
+    const uint32_t rb = L::A + (L::MA == 2 ? (ar >> 3) * 1024 : 0) + (ar & 7) * 128 + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rd_a[j] = rb + 32 * ((j + (ar & 7)) & 3);
+  }
+  constexpr long kMinus8 = (long)0xF8F8F8F8F8F8F8F8ull;
+  float acc[T][EU];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < EU; ++e) acc[t][e] = 0.0f;
+
+  auto compute = [&](int i) {
+    if (wave + KS * i >= nq) return;  // clamped duplicate quad (wave-uniform)
+    const uint32_t sb = lds_addr(ring + (i % S) * L::SLOT);
+    u32x2_t ar[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ar[j] = ds_read2<0, 4>(sb + rd_a[j]);
+    u32x4_t xr[EU];
+    if (XS_MODE == NVE_XS_GROUP32_F32) {
+#pragma unroll
+      for (int e = 0; e < EU; ++e) xr[e] = ds_read128(sb + L::XS + (4 * e + g) * 16);
+    }
+    u32x4_t wr[T], sr[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      wr[t] = ds_read128(sb + L::W + t * 1024 + rd_w);
+      sr[t] = ds_read128(sb + L::SC + t * 256 + nl * 16);
+    }
+    lgkm_wait();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tie(ar[j]);
+    if (XS_MODE == NVE_XS_GROUP32_F32) {
+#pragma unroll
+      for (int e = 0; e < EU; ++e) tie(xr[e]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      tie(wr[t]);
+      tie(sr[t]);
+    }
+    long a[4];
+    v4i_t cm[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] = (long)(((unsigned long)ar[j].y << 32) | ar[j].x);  // rows >= M: row M - 1, never stored
+      const v4i_t z = {0, 0, 0, 0};
+      cm[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], kMinus8, z, 0, 0, 0);
+    }
+    float4 xv[EU];
+    if (XS_MODE == NVE_XS_GROUP32_F32) {
+#pragma unroll
+      for (int e = 0; e < EU; ++e)
+        xv[e] = make_float4(__uint_as_float(xr[e].x), __uint_as_float(xr[e].y), __uint_as_float(xr[e].z),
+                            __uint_as_float(xr[e].w));
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint32_t c0 = wr[t].x, c1 = wr[t].y, c2 = wr[t].z, c3 = wr[t].w;
+      transpose4(c0, c1, c2, c3);
+      const uint32_t cj[4] = {c0, c1, c2, c3};
+      const float scj[4] = {__uint_as_float(sr[t].x), __uint_as_float(sr[t].y), __uint_as_float(sr[t].z),
+                            __uint_as_float(sr[t].w)};
+      v4i_t d[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = cj[j] & 0x0F0F0F0Fu, hi = (cj[j] >> 4) & 0x0F0F0F0Fu;
+        d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], (long)(((unsigned long)hi << 32) | lo), cm[j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < EU; ++e) {
+          float f = scj[j];
+          if (XS_MODE == NVE_XS_GROUP32_F32) f *= (j == 0 ? xv[e].x : j == 1 ? xv[e].y : j == 2 ? xv[e].z : xv[e].w);
+          acc[t][e] = fmaf(f, (float)d[j][e], acc[t][e]);
+        }
+    }
+  };
+
+#pragma unroll
+  for (int i = 0; i < S; ++i) issue(i);
+  int i = 0;
+  for (; i + S < nqw; ++i) {
+    wait_vmcnt<(S - 1) * L::LOADS>();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(i + S);
+  }
+#pragma unroll
+  for (int k = 0; k < S; ++k) {
+    if (k == 0) wait_vmcnt<(S - 1) * L::LOADS>();
+    if (k == 1) wait_vmcnt<(S > 1 ? S - 2 : 0) * L::LOADS>();
+    if (k == 2) wait_vmcnt<(S > 2 ? S - 3 : 0) * L::LOADS>();
+    if (k == 3) wait_vmcnt<(S > 3 ? S - 4 : 0) * L::LOADS>();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i + k);
+  }
+
+  __syncthreads();  // every wave is done with its ring: reuse the LDS for the reduction
+  float(*s_red)[T * 16][4 * EU + 1] = (float(*)[T * 16][4 * EU + 1])smem;
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < EU; ++e) s_red[wave][16 * t + nl][4 * e + g] = acc[t][e];
+  __syncthreads();
+  const int rows = min(rows_per_wg, N - row0);
+  for (int x = threadIdx.x; x < T * 16 * 4 * EU; x += 64 * KS) {
+    const int mm = x / (16 * T), r = x % (16 * T);
+    float y = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < KS; ++w2) y += s_red[w2][r][mm];
+    if (mm < M && r < rows) {
+      if (XS_MODE == NVE_XS_ROW_BF16) y *= bf16_bits_to_f32(((const uint16_t*)xs)[mm]);
+      store_out<OUT_DT>(out, (size_t)mm * N + row0 + r, y);
+    }
+  }
+}
+
 }  // namespace nve
 
 namespace nve_host {
@@ -422,18 +684,67 @@ static hipError_t launch_mfma(int M, const int8_t* xq, const void* xs, const uin
   return hipGetLastError();
 }
 
+// LDS-ring kernel configuration: 16 waves per workgroup, one quad in flight per wave.
+// Measured on the 8B gate (T = 4) and down (T = 1) shapes at M = 4 / 8 / 16 (us):
+//   16 waves, depth 1:                 gate 9.07 / 9.30 / 10.26   down 9.16 / 9.69 / 11.25
+//   16 waves, depth 2 (down):                                     down 9.21 / 10.48 / 12.21
+//   16 waves, depth 3 (down), 8 waves, depth 3 (gate):
+//                                      gate 9.95 / 10.31 / 10.46  down 9.73 / 10.47 / 12.34
+// Deeper rings do not help (sixteen waves already keep 40-118 KiB per CU in flight).
+template <int T, int EU>
+struct RingCfg {
+  static constexpr int KS = 16;
+  static constexpr int S = 1;
+};
+
+template <int OUT_DT, int XS, int T, int EU>
+static hipError_t launch_ring_t(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
+                                void* out, int N, int K, int rpw, hipStream_t stream) {
+  using C = RingCfg<T, EU>;
+  const int nq = K / 128;
+  if ((nq + C::KS - 1) / C::KS < C::S) return hipErrorNotSupported;
+  const int grid = (N + rpw - 1) / rpw;
+  hipLaunchKernelGGL((nve::w4a8_batched_mfma_lds_kernel<OUT_DT, XS, C::KS, T, EU, C::S>), dim3(grid),
+                     dim3(64 * C::KS), 0, stream, M, xq, xs, nib, ws, out, N, K, rpw);
+  return hipGetLastError();
+}
+
+// hipErrorNotSupported: the shape is outside the ring kernel's range (the caller takes
+// the register kernel).
+template <int OUT_DT, int XS, int EU>
+static hipError_t launch_ring(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
+                              void* out, int N, int K, hipStream_t stream) {
+  constexpr int kCU = 256;
+  if (K % 128 != 0 || N > kCU * 64 || !aligned(ws, 4) || !aligned(xq, 16) || !aligned(nib, 16))
+    return hipErrorNotSupported;
+  const int rpw = N <= 16 * kCU ? 16 : (N + kCU - 1) / kCU;
+  switch ((rpw + 15) / 16) {
+    case 1: return launch_ring_t<OUT_DT, XS, 1, EU>(M, xq, xs, nib, ws, out, N, K, rpw, stream);
+    case 2: return launch_ring_t<OUT_DT, XS, 2, EU>(M, xq, xs, nib, ws, out, N, K, rpw, stream);
+    case 3: return launch_ring_t<OUT_DT, XS, 3, EU>(M, xq, xs, nib, ws, out, N, K, rpw, stream);
+    default: return launch_ring_t<OUT_DT, XS, 4, EU>(M, xq, xs, nib, ws, out, N, K, rpw, stream);
+  }
+}
+
 template <int OUT_DT, int XS>
 static hipError_t launch_mfma_m(int M, const int8_t* xq, const void* xs, const uint8_t* nib, const float* ws,
                                 void* out, int N, int K, hipStream_t stream) {
+  {
+    const hipError_t e = M <= 4   ? launch_ring<OUT_DT, XS, 1>(M, xq, xs, nib, ws, out, N, K, stream)
+                         : M <= 8 ? launch_ring<OUT_DT, XS, 2>(M, xq, xs, nib, ws, out, N, K, stream)
+                                  : launch_ring<OUT_DT, XS, 4>(M, xq, xs, nib, ws, out, N, K, stream);
+    if (e != hipErrorNotSupported) return e;
+  }
   if (M <= 4) return launch_mfma<OUT_DT, XS, 1>(M, xq, xs, nib, ws, out, N, K, stream);
   if (M <= 8) return launch_mfma<OUT_DT, XS, 2>(M, xq, xs, nib, ws, out, N, K, stream);
   return launch_mfma<OUT_DT, XS, 4>(M, xq, xs, nib, ws, out, N, K, stream);
 }
 
 // Staged v_dot4 kernel: the one-row GEMV's tiling (R rows per wave, NJ 64-block chunks
-// per lane, one staging pass), the activation rows in LDS.  It serves M = 2 where the
-// two staged rows take at most 40 KB of LDS (8B gate 14336x4096: 9.2 us against 11.3 us
-// on MFMA; down 4096x14336: 10.4 against 10.5).  From M = 3 the per-workgroup staging
+// per lane, one staging pass), the activation rows in LDS.  It serves M = 2 outside the
+// LDS-ring kernel's range where the two staged rows take at most 40 KB of LDS (8B gate
+// 14336x4096: 9.2 us against 11.3 us on the register MFMA kernel; down 4096x14336: 10.4
+// against 10.5).  From M = 3 the per-workgroup staging
 // (every workgroup stages every row) and the M-fold LDS operand reads cost more than the
 // MFMA kernel's transposes (gate M = 4: 12.1 against 11.6 us).
 static constexpr int kStagedM = 2;
@@ -486,6 +797,14 @@ static hipError_t launch_batched_o(int M, const int8_t* xq, const void* xs, int 
     s.n[0] = N;
     if (xs_mode == NVE_XS_ROW_BF16) return launch_w4a8_rowscale(xq, (const uint16_t*)xs, s, OUT_DT, K, stream);
     return launch_w4a8(xq, (const float*)xs, s, OUT_DT, K, stream);
+  }
+  if (M == 2 && batched_use_mfma()) {
+    // the LDS-ring MFMA kernel where it applies (8B gate: 8.9 us against 9.3 on the
+    // staged v_dot4 kernel, down 9.2 against 10.3), else the staged kernel below
+    const hipError_t e = xs_mode == NVE_XS_ROW_BF16
+                             ? launch_ring<OUT_DT, NVE_XS_ROW_BF16, 1>(M, xq, xs, nib, ws, out, N, K, stream)
+                             : launch_ring<OUT_DT, NVE_XS_GROUP32_F32, 1>(M, xq, xs, nib, ws, out, N, K, stream);
+    if (e != hipErrorNotSupported) return e;
   }
   if (staged_fits(M, N, K)) {
     if (xs_mode == NVE_XS_ROW_BF16)
