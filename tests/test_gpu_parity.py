@@ -468,14 +468,16 @@ def test_dispatch_project(orc, torch_dev, hk, monkeypatch):
 
 @pytest.mark.parametrize("m", [2, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("n,k", [(16, 32), (17, 96), (300, 160), (1000, 2048), (8200, 4096), (70, 14336),
-                                 (4096, 14336), (14336, 4096), (6000, 4096), (12000, 4096)])
+                                 (4096, 14336), (14336, 4096), (6000, 4096), (12000, 4096), (4097, 2048),
+                                 (16384, 1024), (16400, 1024)])
 @pytest.mark.parametrize("per_token", [False, True])
 def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
     """M >= 3 runs on the int8 MFMA kernels (M = 2 on the staged v_dot4 kernel where it
     fits): ragged N, K with a partial last block quad (K % 128 != 0: the register kernel
     with scalar scale loads), the LDS-ring kernel at 1-4 tiles per workgroup with a
-    partly masked last tile (6000, 8200, 12000, 14336 rows: 24, 33, 47, 56 rows per
-    workgroup), every live-element count (M = 4, 5-8, 13-16)."""
+    partly masked last tile (4097, 6000, 8200, 12000, 14336 rows: 17, 24, 33, 47, 56 rows
+    per workgroup; 16384 rows: four full tiles, the largest ring shape; 16400 rows: past
+    it, on the register kernel), every live-element count (M = 4, 5-8, 13-16)."""
     torch = torch_dev
     _, _, nib, ws = _problem(orc, n, k, seed=m * 7 + n)
     x = to_bf16(activations(k, seed=300 + m, m=m))
