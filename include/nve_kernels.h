@@ -271,7 +271,8 @@ int nve_hip_set_gemv_policy(int policy, int persistent_wg_per_cu, int persistent
  *   h += o_proj(attn(rope(q), rope(k) ++ K cache, V cache))    with x = rmsnorm(h)
  *   h += down(silu(gate(x2)) * up(x2))                         with x2 = rmsnorm(h)
  * Precision per layer: W4A8 (every GEMV input quantized to int8 with group-32
- * scales, nve_quantize_f16_q8 semantics) or W4A16 (bf16 GEMV inputs).  Five launches
+ * scales, nve_quantize_f16_q8 semantics) or W4A16 (fp16 GEMV inputs, the reference's
+ * decode type).  Five launches
  * per layer: Q/K/V with the RMSNorm computed in its staging; attention (RoPE, cache
  * append, softmax, output converted to the o_proj input -- or, for caches of more than
  * 256 slots, split over 4 workgroups per head (8 above 1024 slots when

@@ -202,6 +202,19 @@ __device__ __forceinline__ int4 prod_quant16(const float (&v)[16], float& scale_
 }
 
 // W4A16: 8 values -> 8 bf16 (round to nearest even), as the standalone producers store.
+// Eight producer values rounded once to fp16 (W4A16 staging in MODE_F16).  The values
+// are formed in f64 and narrowed to f32 first; f32_to_f16_rne keeps that f32 step (left to
+// itself the compiler folds the two truncations into one f64 -> f16 conversion, which
+// gfx950 has no instruction for: a 30-instruction integer sequence per value).
+__device__ __forceinline__ uint4 prod_f16x8(const float (&v)[8]) {
+  uint32_t d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    d[t] = (uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(v[2 * t])) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(v[2 * t + 1])) << 16);
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
 __device__ __forceinline__ uint4 prod_bf16x8(const float (&v)[8]) {
   uint32_t d[4];
 #pragma unroll

@@ -25,11 +25,12 @@ namespace nve {
 // src/ops.rs:12-30, output rounded once.  One workgroup of 1024 threads; thread t
 // handles elements 4t..4t+3 of each 4096-element pass (8 threads per 32-group, so the
 // fused W4A8 quantization is a DPP reduction over 8 lanes).
-// OUT: 0 -> bf16 y; 1 -> int8 xq + f32 group scales (nve_quantize_f16_q8 semantics).
+// OUT: 0 -> fp16 y (a W4A16 layer's input); 1 -> int8 xq + f32 group scales
+// (nve_quantize_f16_q8 semantics).
 template <int OUT>
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ h,
                                                        const uint16_t* __restrict__ w, float eps, int H,
-                                                       uint16_t* __restrict__ y_bf16, int8_t* __restrict__ xq,
+                                                       uint16_t* __restrict__ y16, int8_t* __restrict__ xq,
                                                        float* __restrict__ xs) {
   __shared__ double red[16];
   double ss = 0.0;
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
     if (OUT == 0) {
       if (ok)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) y_bf16[i0 + t] = f32_to_bf16_bits(v[t]);
+        for (int t = 0; t < 4; ++t) ((_Float16*)y16)[i0 + t] = f32_to_f16_rne(v[t]);
     } else {
       q8_group8_store(v, ok, xq, xs, (size_t)(ok ? i0 : 0));
     }
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 // ---- attention ------------------------------------------------------------------
 // One launch per layer: RoPE on q and on the new key, KV-cache append,
 // softmax(q k^T / sqrt(D)) v over the cache, and the conversion of the output to the
-// o_proj input (OUT 1: bf16, OUT 2: int8 + group-32 scales).
+// o_proj input (OUT 1: fp16, OUT 2: int8 + group-32 scales).
 //
 // One workgroup of 16 waves per query head; no cross-workgroup communication.  Keys
 // are spread over the waves in tiles: a key's row of D bf16 (D/8 16-byte pieces)
@@ -166,11 +167,11 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
 }
 
 // Merge of the 16 wave states of an attention workgroup and its output: the normalised
-// head output converted to the o_proj input (OUT 1: bf16, 2: int8 + group scales), or
+// head output converted to the o_proj input (OUT 1: fp16, 2: int8 + group scales), or
 // (OUT 3) the split's partial record (m, l, 0, 0, acc[D]).
 template <int D, int OUT, int SPLIT>
 __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&acc)[8], int hq, int sp, int num_heads,
-                                            int wave, int krow, int col, int tid, float* s_m, float* s_l, float* s_acc, uint16_t* __restrict__ out_bf16,
+                                            int wave, int krow, int col, int tid, float* s_m, float* s_l, float* s_acc, uint16_t* __restrict__ out16,
                                             int8_t* __restrict__ out_q, float* __restrict__ out_s,
                                             float* __restrict__ out_part) {
   using T = AttnTile<D>;
@@ -226,7 +227,7 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
     const size_t i0 = (size_t)hq * D + 4 * tid;
     if (OUT == 1) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) out_bf16[i0 + e] = f32_to_bf16_bits(o[e]);
+      for (int e = 0; e < 4; ++e) ((_Float16*)out16)[i0 + e] = f32_to_f16_rne(o[e]);
     } else {
       q8_group8_store(o, true, out_q, out_s, i0);
     }
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
-    int max_seq, float qscale, uint16_t* __restrict__ out_bf16, int8_t* __restrict__ out_q,
+    int max_seq, float qscale, uint16_t* __restrict__ out16, int8_t* __restrict__ out_q,
     float* __restrict__ out_s, float* __restrict__ out_part, int xcd_map) {
   static_assert((OUT == 3) == (SPLIT > 1), "split partials go to out_part");
   using T = AttnTile<D>;
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
       attn_compute<D, false>(b1, sp + SPLIT * (j + 4), len, pos, wave, krow, col, qv, s_knew, s_vnew, m_run, l_run,
                              acc);
     attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_acc,
-                               out_bf16, out_q, out_s, out_part);
+                               out16, out_q, out_s, out_part);
     return;
   }
   // q, k, v of this head before the position-dependent RoPE rows
@@ -394,15 +395,15 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     if (j + 5 < nt) attn_issue<D>(b2, kc, vc, cache_base, sp + SPLIT * (j + 5), len, wave, krow, col);
   }
   attn_finish<D, OUT, SPLIT>(m_run, l_run, acc, hq, sp, num_heads, wave, krow, col, tid, s_m, s_l, s_acc,
-                             out_bf16, out_q, out_s, out_part);
+                             out16, out_q, out_s, out_part);
 }
 
 // ---- SiLU * up ------------------------------------------------------------------
-// mid = silu(gate) * up (src/ops.rs:62-64: g / (1 + exp(-g))).  OUT 0 -> bf16,
+// mid = silu(gate) * up (src/ops.rs:62-64: g / (1 + exp(-g))).  OUT 0 -> fp16,
 // 1 -> int8 + group scales (fused W4A8 quantization; 8 lanes per 32-group).
 template <int OUT>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
-                                                       int F, uint16_t* __restrict__ y_bf16, int8_t* __restrict__ xq,
+                                                       int F, uint16_t* __restrict__ y16, int8_t* __restrict__ xq,
                                                        float* __restrict__ xs) {
   const int i0 = 4 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
   const bool ok = i0 < F;  // F % 32 == 0
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
   if (OUT == 0) {
     if (ok)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) y_bf16[i0 + t] = f32_to_bf16_bits(v[t]);
+      for (int t = 0; t < 4; ++t) ((_Float16*)y16)[i0 + t] = f32_to_f16_rne(v[t]);
   } else {
     q8_group8_store(v, ok, xq, xs, (size_t)ib);
   }
@@ -554,7 +555,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
 namespace nve_host {
 
 struct DecodeWs {
-  uint16_t* act_bf16;  // [max(H, Hq*D, F)]
+  uint16_t* act16;  // [max(H, Hq*D, F)]
   int8_t* xq;          // [max(H, Hq*D, F)]
   float* xs;           // [max/32]
   float* q;            // [Hq*D]
@@ -594,7 +595,7 @@ static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
     off += align256(bytes);
     return r;
   };
-  w.act_bf16 = (uint16_t*)take(mx * 2);
+  w.act16 = (uint16_t*)take(mx * 2);
   w.xq = (int8_t*)take(mx);
   w.xs = (float*)take(mx / 32 * 4);
   w.q = (float*)take(qd * 4);
@@ -662,7 +663,7 @@ static hipError_t launch_rmsnorm(const nve_decode_config& c, const float* h, con
     hipLaunchKernelGGL(nve::rmsnorm_kernel<1>, dim3(1), dim3(1024), 0, s, h, w, c.eps, c.hidden, nullptr, ws.xq,
                        ws.xs);
   else
-    hipLaunchKernelGGL(nve::rmsnorm_kernel<0>, dim3(1), dim3(1024), 0, s, h, w, c.eps, c.hidden, ws.act_bf16,
+    hipLaunchKernelGGL(nve::rmsnorm_kernel<0>, dim3(1), dim3(1024), 0, s, h, w, c.eps, c.hidden, ws.act16,
                        nullptr, nullptr);
   return hipGetLastError();
 }
@@ -679,7 +680,7 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
 #define NVE_ATTN_P(D, OUT, S, P)                                                                             \
   hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S, P>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
                      ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,                \
-                     c.num_kv_heads, c.max_seq, qscale, ws.act_bf16, ws.xq, ws.xs, ws.part, xcd_map)
+                     c.num_kv_heads, c.max_seq, qscale, ws.act16, ws.xq, ws.xs, ws.part, xcd_map)
 #define NVE_ATTN(D, OUT, S)          \
   if (pre) NVE_ATTN_P(D, OUT, S, true); \
   else NVE_ATTN_P(D, OUT, S, false);
@@ -728,7 +729,7 @@ static bool decode_fuse() {
 
 static hipError_t gemv(bool w4a8, const DecodeWs& ws, const W4Segs& sg, int out_dt, int K, hipStream_t s) {
   return w4a8 ? launch_w4a8(ws.xq, ws.xs, sg, out_dt, K, s)
-              : launch_w4a16(ws.act_bf16, NVE_DT_BF16, sg, out_dt, K, s);
+              : launch_w4a16(ws.act16, NVE_DT_F16, sg, out_dt, K, s);
 }
 
 static hipError_t gemv_fused(bool w4a8, int src, int pair, const nve::ProdArgs& pa, const W4Segs& sg, int out_dt,
@@ -811,7 +812,7 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
       NVE_TRY(gemv(w4a8, ws, sg, NVE_DT_F32, H, s));
     }
   }
-  // attention writes the o_proj input directly (int8 + scales, or bf16), or, split over
+  // attention writes the o_proj input directly (int8 + scales, or fp16), or, split over
   // the keys, partials that the o_proj staging merges
   const int split = fuse ? attn_split(c) : 1;
   NVE_TRY(launch_attention(c, io, ws, w4a8, split, fuse, s));
@@ -823,14 +824,14 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
     NVE_TRY(gemv(w4a8, ws, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
   // FFN sub-layer: norm -> gate/up (one grouped launch) -> silu*up -> down (+h).  Fused:
   // the gate/up launch pairs the rows of both matrices and writes silu(gate) * up
-  // (f32 for W4A8, whose down GEMV quantizes it in its staging; bf16 for W4A16).
+  // (f32 for W4A8, whose down GEMV quantizes it in its staging; fp16 for W4A16).
   {
     const nve_w4_weight gu[2] = {w.gate, w.up};
     if (fuse) {
-      void* outs[2] = {w4a8 ? (void*)ws.gate : (void*)ws.act_bf16, nullptr};
+      void* outs[2] = {w4a8 ? (void*)ws.gate : (void*)ws.act16, nullptr};
       const W4Segs sg = segs3(gu, outs, 2);
       NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_SWIGLU, nve::ProdArgs{io.hidden, w.post_attn_norm, c.eps}, sg,
-                         w4a8 ? NVE_DT_F32 : NVE_DT_BF16, H, s));
+                         w4a8 ? NVE_DT_F32 : NVE_DT_F16, H, s));
       if (w4a8)
         NVE_TRY(gemv_fused(true, nve::SRC_F32, nve::PAIR_NONE, nve::ProdArgs{ws.gate, nullptr, 0.0f},
                            one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
@@ -847,7 +848,7 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
   if (w4a8)
     hipLaunchKernelGGL(nve::silu_mul_kernel<1>, sgrid, dim3(256), 0, s, ws.gate, ws.up, F, nullptr, ws.xq, ws.xs);
   else
-    hipLaunchKernelGGL(nve::silu_mul_kernel<0>, sgrid, dim3(256), 0, s, ws.gate, ws.up, F, ws.act_bf16, nullptr,
+    hipLaunchKernelGGL(nve::silu_mul_kernel<0>, sgrid, dim3(256), 0, s, ws.gate, ws.up, F, ws.act16, nullptr,
                        nullptr);
   NVE_TRY(hipGetLastError());
   NVE_TRY(gemv(w4a8, ws, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
@@ -864,7 +865,7 @@ int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8
     NVE_TRY(launch_w4a8(ws.xq, ws.xs, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
   } else {
     NVE_TRY(launch_rmsnorm(c, hd.hidden, hd.final_norm, w4a8, ws, s));
-    NVE_TRY(launch_w4a16(ws.act_bf16, NVE_DT_BF16, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
+    NVE_TRY(launch_w4a16(ws.act16, NVE_DT_F16, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
   }
   hipLaunchKernelGGL(nve::argmax_partial_kernel, dim3(nve::kArgmaxBlocks), dim3(256), 0, s, logits, hd.lm_head.n,
                      ws.arg_v, ws.arg_i);

@@ -208,7 +208,7 @@ __device__ __forceinline__ double stage_sumsq(const ProdChunk<SRC, E> (&pc)[SPT]
 
 template <bool W4A8>
 __host__ __device__ constexpr size_t stage_bytes(int K) {
-  return W4A8 ? w4a8_lds_bytes(K) : w4a16_lds_bytes(MODE_BF16, K);
+  return W4A8 ? w4a8_lds_bytes(K) : w4a16_lds_bytes(MODE_F16, K);
 }
 
 // Issue the staging loads of one phase (compute waves).
@@ -243,7 +243,7 @@ __device__ __forceinline__ void stage_write(const ProdChunk<SRC, E> (&pc)[SPT], 
       const int i = (int)threadIdx.x + NT * s;
       float v[8];
       prod_values<SRC, 8>(pc[s], inv, v);
-      w4a16_stage_put_dot<MODE_BF16>(prod_bf16x8(v), i, i < nchunk, nb, (int*)lds, (float*)(lds + 4 * (nb + 1)));
+      w4a16_stage_put_dot<MODE_F16>(prod_f16x8(v), i, i < nchunk, nb, (int*)lds, nullptr);
     }
   }
 }
@@ -276,12 +276,11 @@ __device__ __forceinline__ void gemv_dot(const WBuf<R, NJ>& b, const int4* lds, 
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     const int ps = nb + 1;
-    const float* s_mul = (const float*)(lds + 4 * ps);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int bi = lane + 64 * j;
       const int bb = min(bi, nb - 1);
-      const float mul = bi < nb ? s_mul[bb] : 0.0f;
+      const float mul = bi < nb ? 1.0f : 0.0f;  // fp16 staging: no block multiplier
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const float s = w4a16_block_dot_h(b.w[r][j], lds, ps, bb, magic);

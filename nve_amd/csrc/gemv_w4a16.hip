@@ -36,8 +36,9 @@
 
 namespace nve {
 
-// SRC != SRC_PLAIN (MODE_BF16 only): the activations are computed in the staging
-// from the producer's inputs (act_producer.h) and rounded to bf16.
+// SRC != SRC_PLAIN (MODE_F16 only): the activations are computed in the staging from
+// the producer's inputs (act_producer.h) and rounded to fp16, the activation type of the
+// reference's decode path (its W4A16 kernel takes fp16 x, src/cuda_kernels.rs:117-126).
 // PAIR (act_producer.h): PAIR_SWIGLU -- segment 0 (gate) and the matrix in nib[1] /
 // sc[1] (up) share N; a wave computes R/2 rows of each and writes silu(gate) * up
 // (src/ops.rs:62-64).  PAIR_ROPE -- segments q, k, v, each N = rows / 2 pairs; a wave
@@ -46,7 +47,7 @@ template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = SR
 __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict__ x, W4Segs segs,
                                                          int K, ProdArgs pa, RopeArgs ra) {
   constexpr bool SWI = PAIR == PAIR_SWIGLU, ROPE = PAIR == PAIR_ROPE;
-  static_assert(SRC == SRC_PLAIN || (!MULTI && MODE == MODE_BF16), "fused producers: one-pass bf16 staging");
+  static_assert(SRC == SRC_PLAIN || (!MULTI && MODE == MODE_F16), "fused producers: one-pass fp16 staging");
   static_assert(PAIR == PAIR_NONE || (R % 2 == 0 && !MULTI && MODE != MODE_F32), "paired rows: even R, one pass");
   constexpr int RH = PAIR != PAIR_NONE ? R / 2 : R;  // output rows (pairs) per wave
   constexpr int SPT = NJ;  // staging passes: K/8 chunks <= 256*NJ
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       const int i = (int)threadIdx.x + 256 * s;
       float v[8];
       prod_values<SRC, 8>(pc[s], inv, v);
-      w4a16_stage_put_dot<MODE>(prod_bf16x8(v), i, i < nchunk, nb, s_p, s_mul);
+      w4a16_stage_put_dot<MODE>(prod_f16x8(v), i, i < nchunk, nb, s_p, s_mul);
     }
     if (kLateWeights && SRC != SRC_NORM) issue_pinned();
   } else if (!MULTI) {
@@ -280,7 +281,7 @@ static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int
     finalize_segments(segs, R / 2);
 #define NVE_W4A16_PAIR_CASE(RR, JJ) \
     if (R == RR && t.NJ == JJ) \
-      return launch_w4a16_t<nve::MODE_BF16, NVE_DT_BF16, OUT_DT, RR, JJ, false, SRC, PAIR>(nullptr, segs, K, stream, pa, ra);
+      return launch_w4a16_t<nve::MODE_F16, NVE_DT_F16, OUT_DT, RR, JJ, false, SRC, PAIR>(nullptr, segs, K, stream, pa, ra);
     NVE_W4_SWIGLU_CASES(NVE_W4A16_PAIR_CASE)
 #undef NVE_W4A16_PAIR_CASE
     return hipErrorInvalidValue;
@@ -288,7 +289,7 @@ static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int
   finalize_segments(segs, t.R);
 #define NVE_W4A16_CASE(RR, JJ, MM) \
   if (t.R == RR && t.NJ == JJ && !MM) \
-    return launch_w4a16_t<nve::MODE_BF16, NVE_DT_BF16, OUT_DT, RR, JJ, false, SRC>(nullptr, segs, K, stream, pa);
+    return launch_w4a16_t<nve::MODE_F16, NVE_DT_F16, OUT_DT, RR, JJ, false, SRC>(nullptr, segs, K, stream, pa);
   NVE_W4_TILING_CASES(NVE_W4A16_CASE)
 #undef NVE_W4A16_CASE
   return hipErrorInvalidValue;
@@ -321,11 +322,11 @@ hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt,
   }
 }
 
-// Decode-layer W4A16 GEMVs with a fused producer (act_producer.h), bf16 staging:
+// Decode-layer W4A16 GEMVs with a fused producer (act_producer.h), fp16 staging:
 //   NORM, F32, rope    Q/K/V from the residual and the norm weights, RoPE + KV append
 //                      in the epilogue (PAIR_ROPE);
 //   NORM, F32          Q/K/V from the residual and the norm weights;
-//   NORM, BF16, swiglu gate/up -> silu(gate) * up rounded to bf16 (the down input);
+//   NORM, F16, swiglu  gate/up -> silu(gate) * up rounded to fp16 (the down input);
 //   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
 hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                               hipStream_t stream, const nve::RopeArgs& ra) {
@@ -333,8 +334,8 @@ hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const 
     return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_ROPE>(pa, segs, K, stream, ra);
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && pair == nve::PAIR_NONE)
     return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_NONE>(pa, segs, K, stream, ra);
-  if (src == nve::SRC_NORM && out_dt == NVE_DT_BF16 && pair == nve::PAIR_SWIGLU)
-    return launch_w4a16_fused_t<NVE_DT_BF16, nve::SRC_NORM, nve::PAIR_SWIGLU>(pa, segs, K, stream, ra);
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F16 && pair == nve::PAIR_SWIGLU)
+    return launch_w4a16_fused_t<NVE_DT_F16, nve::SRC_NORM, nve::PAIR_SWIGLU>(pa, segs, K, stream, ra);
   if (pair != nve::PAIR_NONE || out_dt != NVE_DT_F32_ACCUM) return hipErrorInvalidValue;
   if (src == nve::SRC_ATTN2) return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN2, nve::PAIR_NONE>(pa, segs, K, stream, ra);
   if (src == nve::SRC_ATTN4) return launch_w4a16_fused_t<NVE_DT_F32_ACCUM, nve::SRC_ATTN4, nve::PAIR_NONE>(pa, segs, K, stream, ra);

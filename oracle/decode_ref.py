@@ -3,7 +3,8 @@
 Two uses:
   * `emulate_step` -- the checker for nve_amd.decode: the same layer math as the HIP
     path (W4A8 layers quantize their activations with the group-32 quantizer,
-    W4A16 layers see bf16 activations; bf16 KV cache; fp32 residual), evaluated with
+    W4A16 layers see fp16 activations as the reference's decode path does, whose W4A16
+    kernel takes fp16 x, src/cuda_kernels.rs:117-126; bf16 KV cache; fp32 residual), evaluated with
     float64 dot products on the oracle's restated kernels.
   * `reference_step` -- the reference's CPU decode path for the bench's CPU baseline:
     every projection through QuantizedTensor::matvec_f32 (src/quantize.rs:466-488,
@@ -28,6 +29,12 @@ def bf16_round(x) -> np.ndarray:
     u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
     return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_round(x) -> np.ndarray:
+    """f32 -> fp16 -> f32: round to nearest even, fp16 subnormals kept, overflow to inf
+    (what the W4A16 staging's v_cvt_f16_f32 does)."""
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
 
 
 def bf16_to_f32(bits) -> np.ndarray:
@@ -128,7 +135,7 @@ def _gemv_emulated(x: np.ndarray, wt, w4a8: bool) -> np.ndarray:
     if w4a8:
         q, s = orc.quantize_q8_group(x.astype(F32))
         return orc.matvec_w4a8_f64(q, s, nib, sc, n, k).astype(F32)
-    return orc.matvec_w4a16_f64(bf16_round(x), nib, sc, n, k).astype(F32)
+    return orc.matvec_w4a16_f64(f16_round(x), nib, sc, n, k).astype(F32)
 
 
 def emulate_layer(hm: HostModel, li: int, h: np.ndarray, pos: int) -> np.ndarray:

@@ -93,6 +93,20 @@ def test_silu_known_values(dr):
     assert np.allclose(dr.silu(x), [0.0, 1 / (1 + math.exp(-1)), -1 / (1 + math.e), 20.0], rtol=1e-6)
 
 
+def test_activation_roundings_known_answers(dr):
+    """bf16 (KV cache, W4A8 staging inputs) and fp16 (W4A16 activations) rounding: ties
+    to even, the last finite values, overflow and fp16 subnormals, by value."""
+    bmax = (2 - 2.0 ** -7) * 2.0 ** 127  # largest finite bf16
+    b = dr.bf16_round(np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, 1 + 2.0 ** -9, -2.5, bmax, 0.0], np.float32))
+    assert b.tolist() == [1.0, 1 + 2.0 ** -6, 1.0, -2.5, bmax, 0.0]
+    h = dr.f16_round(np.array([1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, 65504.0, 65520.0, -65520.0, 2.0 ** -24,
+                               2.0 ** -25, 3 * 2.0 ** -26, 0.1], np.float32))
+    assert h[:3].tolist() == [1.0, 1 + 2.0 ** -9, 65504.0]
+    assert h[3] == np.inf and h[4] == -np.inf
+    assert h[5:8].tolist() == [2.0 ** -24, 0.0, 2.0 ** -24]
+    assert h[8] == np.float32(0.0999755859375)  # 0x2E66
+
+
 def test_precision_mask_counts_and_seed():
     from nve_amd.decode import precision_mask
     m = precision_mask(28, 0.3, 7)
