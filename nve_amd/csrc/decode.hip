@@ -399,8 +399,9 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
 }
 
 // ---- SiLU * up ------------------------------------------------------------------
-// mid = silu(gate) * up (src/ops.rs:62-64: g / (1 + exp(-g))).  OUT 0 -> fp16,
-// 1 -> int8 + group scales (fused W4A8 quantization; 8 lanes per 32-group).
+// mid = silu(gate) * up (src/ops.rs:62-64: g / (1 + exp(-g))) rounded to fp16.  OUT 0 ->
+// fp16, 1 -> int8 + group scales of the fp16 values (fused W4A8 quantization; 8 lanes per
+// 32-group).
 template <int OUT>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                        int F, uint16_t* __restrict__ y16, int8_t* __restrict__ xq,
@@ -413,7 +414,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
   const float gg[4] = {g4.x, g4.y, g4.z, g4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
   float v[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) v[t] = gg[t] / (1.0f + expf(-gg[t])) * uu[t];
+  for (int t = 0; t < 4; ++t) v[t] = (float)f32_to_f16_rne(gg[t] / (1.0f + expf(-gg[t])) * uu[t]);
   if (OUT == 0) {
     if (ok)
 #pragma unroll
@@ -824,16 +825,17 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
     NVE_TRY(gemv(w4a8, ws, one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
   // FFN sub-layer: norm -> gate/up (one grouped launch) -> silu*up -> down (+h).  Fused:
   // the gate/up launch pairs the rows of both matrices and writes silu(gate) * up
-  // (f32 for W4A8, whose down GEMV quantizes it in its staging; fp16 for W4A16).
+  // rounded to fp16, as the reference's candle FFN holds it (src/gpu_layer.rs:937-946);
+  // the W4A8 down GEMV quantizes it in its staging, the W4A16 one reads it as is.
   {
     const nve_w4_weight gu[2] = {w.gate, w.up};
     if (fuse) {
-      void* outs[2] = {w4a8 ? (void*)ws.gate : (void*)ws.act16, nullptr};
+      void* outs[2] = {(void*)ws.act16, nullptr};
       const W4Segs sg = segs3(gu, outs, 2);
       NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_SWIGLU, nve::ProdArgs{io.hidden, w.post_attn_norm, c.eps}, sg,
-                         w4a8 ? NVE_DT_F32 : NVE_DT_F16, H, s));
+                         NVE_DT_F16, H, s));
       if (w4a8)
-        NVE_TRY(gemv_fused(true, nve::SRC_F32, nve::PAIR_NONE, nve::ProdArgs{ws.gate, nullptr, 0.0f},
+        NVE_TRY(gemv_fused(true, nve::SRC_F16, nve::PAIR_NONE, nve::ProdArgs{ws.act16, nullptr, 0.0f},
                            one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
       else
         NVE_TRY(gemv(false, ws, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));

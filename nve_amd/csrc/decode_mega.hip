@@ -232,6 +232,10 @@ __device__ __forceinline__ void stage_write(const ProdChunk<SRC, E> (&pc)[SPT], 
       const int i = (int)threadIdx.x + NT * s;
       float v[16];
       prod_values<SRC, 16>(pc[s], inv, v);
+      if constexpr (SRC == SRC_F32) {  // the SwiGLU output, held in fp16 as in the launches
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (float)f32_to_f16_rne(v[k]);
+      }
       float scale;
       const int4 q = prod_quant16(v, scale);
       w4a8_stage_put(q, scale, i, i < nchunk, nb, s_lo, s_hi, s_bs);

@@ -110,7 +110,10 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   // the gate/up launch of the 3B decode step: the norm statistic at 3.8 us median with
   // the weights issued first, 2.0 us with them issued after it, kernel end 7.4 -> 6.6
   // us).  The attention-merge producers keep the early issue (late was measured slower).
-  constexpr bool kLateWeights = SRC == SRC_NORM || SRC == SRC_F32;
+  // The decode step's down projection (fp16 SwiGLU output, residual add) is such a
+  // just-written vector too.
+  constexpr bool kLateWeights =
+      SRC == SRC_NORM || SRC == SRC_F32 || (SRC == SRC_F16 && OUT_DT == NVE_DT_F32_ACCUM);
   if (!kLateWeights) issue(0);
   // A late issue is fenced on both sides so that the loads leave as one group at that
   // point: left to itself the scheduler spreads them through the quantization and hoists
@@ -326,6 +329,8 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
 //   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
 hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                              hipStream_t stream, const nve::RopeArgs& ra) {
+  if (src == nve::SRC_NORM && out_dt == NVE_DT_F16 && pair == nve::PAIR_SWIGLU)
+    return launch_w4a8_fused_t<NVE_DT_F16, nve::SRC_NORM, nve::PAIR_SWIGLU>(pa, segs, K, stream, ra);
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32) {
     if (pair == nve::PAIR_ROPE)
       return launch_w4a8_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_ROPE>(pa, segs, K, stream, ra);
@@ -335,6 +340,7 @@ hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W
   if (pair != nve::PAIR_NONE) return hipErrorInvalidValue;
 #define NVE_FU(SRC, OD) launch_w4a8_fused_t<OD, SRC, nve::PAIR_NONE>(pa, segs, K, stream, ra)
   if (src == nve::SRC_F32 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_F32, NVE_DT_F32_ACCUM);
+  if (src == nve::SRC_F16 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_F16, NVE_DT_F32_ACCUM);
   if (src == nve::SRC_ATTN2 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_ATTN2, NVE_DT_F32_ACCUM);
   if (src == nve::SRC_ATTN4 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_ATTN4, NVE_DT_F32_ACCUM);
   if (src == nve::SRC_ATTN8 && out_dt == NVE_DT_F32_ACCUM) return NVE_FU(nve::SRC_ATTN8, NVE_DT_F32_ACCUM);

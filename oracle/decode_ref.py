@@ -159,7 +159,7 @@ def emulate_layer(hm: HostModel, li: int, h: np.ndarray, pos: int) -> np.ndarray
     x2 = rms_norm(h, lw["post_attn_norm"], s.eps)
     gt = _gemv_emulated(x2, lw["gate"], w8)
     up = _gemv_emulated(x2, lw["up"], w8)
-    mid = (silu(gt) * up).astype(F32)
+    mid = f16_round(silu(gt) * up)  # held in fp16 (src/gpu_layer.rs:937-946)
     return (h + _gemv_emulated(mid, lw["down"], w8)).astype(F32)
 
 
