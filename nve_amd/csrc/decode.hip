@@ -188,6 +188,41 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
     }
   }
   lds_barrier();
+  if constexpr (OUT == 3) {
+    // split partial record (m, l, 0, 0, acc[D]): the first D / 32 waves merge, lane l of
+    // wave w owning column 32 w + l % 32 and the waves' halves l / 32 (8 of the 16 wave
+    // states each); the two halves meet through one xor-32 lane exchange.  Every lane
+    // forms M and the weights 2^(m_w - M) itself from the broadcast maxima.
+    static_assert(D % 32 == 0 && T::NW % 2 == 0, "merge layout");
+    if (wave < D / 32) {
+      const int lane = tid & 63, c = 32 * wave + (lane & 31), h = lane >> 5;
+      float mw[T::NW];
+#pragma unroll
+      for (int w = 0; w < T::NW; w += 4) {
+        const float4 m4 = *(const float4*)&s_m[w];
+        mw[w] = m4.x, mw[w + 1] = m4.y, mw[w + 2] = m4.z, mw[w + 3] = m4.w;
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < T::NW; ++w) M = fmaxf(M, mw[w]);
+      constexpr int HW = T::NW / 2;
+      float L = 0.0f, o = 0.0f;
+#pragma unroll
+      for (int k = 0; k < HW; ++k) {
+        const int w = h * HW + k;
+        const float mk = s_m[w];  // not mw[w]: a lane-dependent index would put mw in LDS
+        const float f = mk == -INFINITY ? 0.0f : exp2f(mk - M);
+        L = fmaf(f, s_l[w], L);
+        o = fmaf(f, s_acc[w * D + c], o);
+      }
+      L += __shfl_xor(L, 32);
+      o += __shfl_xor(o, 32);
+      float* rec = out_part + ((size_t)sp * num_heads + hq) * (D + 4);
+      if (tid == 0) *(float4*)rec = make_float4(M, L, 0.0f, 0.0f);
+      if (h == 0) rec[4 + c] = o;
+    }
+    return;
+  }
   // one barrier: every output lane reads the 16 wave maxima and sums, forms the wave
   // weights 2^(m_w - M) itself (independent exp2, no second LDS round trip) and sums the
   // 16 wave accumulators of its 4 columns
@@ -214,12 +249,6 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
       o[1] = fmaf(f, a4.y, o[1]);
       o[2] = fmaf(f, a4.z, o[2]);
       o[3] = fmaf(f, a4.w, o[3]);
-    }
-    if (OUT == 3) {
-      float* rec = out_part + ((size_t)sp * num_heads + hq) * (D + 4);
-      if (tid == 0) *(float4*)rec = make_float4(M, L, 0.0f, 0.0f);
-      *(float4*)(rec + 4 + 4 * tid) = make_float4(o[0], o[1], o[2], o[3]);
-      return;
     }
     const float invL = 1.0f / L;
 #pragma unroll
