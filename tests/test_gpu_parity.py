@@ -493,6 +493,42 @@ def test_w4a8_batched_mfma_shapes(orc, torch_dev, hk, m, n, k, per_token):
         assert rel_err_floor(y[r], ref) <= TOL_W4A8, r
 
 
+@pytest.mark.parametrize("per_token", [False, True])
+def test_w4a8_batched_graph_replay_matches_eager(orc, torch_dev, hk, per_token):
+    """The batched kernels (M = 2 and 5 on the LDS-ring kernel, 16 rows on it at T = 2,
+    M = 3 on the register kernel at K % 128 != 0) captured in one HIP graph and replayed
+    several times, with eager work in between: every replay equals the eager result."""
+    torch = torch_dev
+    cases = []
+    for m, n, k in ((2, 6000, 4096), (5, 6000, 4096), (16, 6000, 4096), (3, 300, 160)):
+        _, _, nib, ws = _problem(orc, n, k, seed=m + n)
+        x = to_bf16(activations(k, seed=50 + m, m=m))
+        xq, xs = hk.quantize_q8_rows(up(torch, x).to(torch.bfloat16), per_token=per_token)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        cases.append((xq, xs, up(torch, nib), up(torch, ws), n, k, out))
+
+    def step():
+        for xq, xs, nib, ws, n, k, out in cases:
+            hk.matvec_w4a8_batched(xq, xs, nib, ws, n, k, out=out)
+    step()
+    torch.cuda.synchronize()
+    eager = [c[-1].clone() for c in cases]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(3):
+        for c in cases:
+            c[-1].fill_(float("nan"))
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+        for c in cases:
+            c[-1].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[-1], e)
+
+
 # ---------------------------------------------------------------------------
 # W4A8 GEMV with the activation quantization fused in (nve_hip_matvec_w4a8_x)
 # ---------------------------------------------------------------------------
