@@ -395,14 +395,13 @@ __global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_kernel(int M, const
 
 
 // ---------------------------------------------------------------------------
-// LDS-ring int8 MFMA kernel (M >= 3, K % 128 == 0, N <= 256 * 64).
+// LDS-ring int8 MFMA kernel (M >= 2, K % 128 == 0, N <= 256 * 64).
 //
 // Same operand mapping as the kernel above; what changes is how the bytes reach the
 // operand lanes.  The register kernel moves every loaded dword to its operand lane
-// with ds_bpermute and holds its loads in VGPRs, and its per-quad instruction count
-// (about 200 per wave and quad at one tile) makes it issue-bound.  Here every load is
-// a global -> LDS transfer (global_load_lds, no VGPRs in flight) into a per-wave ring
-// of S slots, each holding one K quad:
+// with ds_bpermute (about 200 instructions per wave and quad at one tile) and holds its
+// loads in VGPRs.  Here every load is a global -> LDS transfer (global_load_lds, no
+// VGPRs in flight) into a per-wave ring of S slots, each holding one K quad:
 //   W  T x 1 KiB   weight tile t, the row-major load layout (16 rows x 64 B, 4 lanes per row)
 //   SC T x 256 B   the tile's 16 x 4 block scales (row-major)
 //   A  MA x 1 KiB  activation rows 8a..8a+7, 128 B each (blocks 4q..4q+3)
@@ -415,9 +414,10 @@ __global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_kernel(int M, const
 // (8-way and 16-way conflicts on the CU's shared LDS, which bound the kernel); the
 // sources are swizzled instead -- load lane (row a, slot s) fetches weight piece
 // (s - a / 2) & 3, activation row m's blocks are rotated by m % 4 -- so each transfer
-// still covers whole rows (coalesced) and the operand reads are conflict-free.  The issue is unconditional (quads past the wave's share are clamped
-// to the last quad) so every quad is the same number of loads and the waits are exact
-// vmcnt immediates: S quads in flight through the steady loop, an unrolled drain.
+// still covers whole rows (coalesced) and the operand reads are conflict-free.
+// The issue is unconditional (quads past the wave's share are clamped to the last
+// quad), so every quad is the same number of transfers and the waits are exact vmcnt
+// immediates: S quads in flight through the steady loop, an unrolled drain.
 // Workgroups take ceil(N / 256) consecutive rows each (T = ceil(rows / 16) tiles, the
 // last one partly masked), so the grid is at most one workgroup per CU and every CU
 // streams the same number of weight bytes; masked lanes issue no loads.
@@ -498,7 +498,9 @@ __global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_lds_kernel(int M, c
   for (int t = 0; t < T; ++t) {
     const int rr = 16 * t + lr;
     const int r = min(row0 + rr, N - 1);
-    wok[t] = (rr < rows_per_wg && row0 + rr < N) || lane == 0;  // lane 0 keeps every transfer issued
+    // masked lanes load nothing; lane 0 always loads (a clamped row if need be), so no
+    // transfer is skipped by the whole wave and the vmcnt immediates stay exact
+    wok[t] = (rr < rows_per_wg && row0 + rr < N) || lane == 0;
     wsrc[t] = nib + (size_t)r * (K >> 1) + 16 * ((lp - (lr >> 1)) & 3);  // swizzled piece
     ssrc[t] = ws + (size_t)r * nb + lp;
   }
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(64 * KS) void w4a8_batched_mfma_lds_kernel(int M, c
 #pragma unroll
   for (int a = 0; a < L::MA; ++a) {
     const int m = 8 * a + (lane >> 3);
-    aok[a] = m < M;
+    aok[a] = m < M;  // lane 0 holds row 0, or row 8 where a second transfer exists (M > 8)
     asrc[a] = xq + (size_t)min(m, M - 1) * K + 16 * (((lane & 7) - 2 * (lane >> 3)) & 7);  // rotated blocks
   }
   const float* xsrc = (const float*)xs + (size_t)min(lr, M - 1) * nb + lp;
