@@ -95,6 +95,14 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       }
     }
   }
+  // Residual add (F32_ACCUM): the output rows' current values are fetched with the
+  // staging loads rather than by a dependent load in the epilogue (one writer per row).
+  constexpr bool ACC = OUT_DT == NVE_DT_F32_ACCUM;
+  float prev[ACC ? RH : 1];
+  if constexpr (ACC) {
+#pragma unroll
+    for (int r = 0; r < RH; ++r) prev[r] = ((const float*)out)[min(row0 + r, N - 1)];
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // (2) weight loads
@@ -230,7 +238,12 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float v = wave_sum_to_lane63(acc[r]);
-      if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+      if (lane == 63 && row0 + r < N) {
+        if constexpr (ACC)
+          ((float*)out)[row0 + r] = prev[r] + v;
+        else
+          store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+      }
     }
   }
 }

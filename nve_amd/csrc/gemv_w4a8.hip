@@ -76,6 +76,17 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   } else if (!MULTI) {
     w4a8_stage_issue<SPT>(st, xq, xs, nchunk, pa.row_scale != nullptr);
   }
+  // Residual add (F32_ACCUM): the output rows' current values are fetched here, with
+  // the staging loads, instead of by a dependent load in the epilogue.  The residual
+  // was written by the previous launch and that load would otherwise add a full
+  // memory round trip to the end of the kernel.  Each row has one writer (lane 63 of
+  // its wave), so the read-add-write stays race-free.
+  constexpr bool ACC = OUT_DT == NVE_DT_F32_ACCUM;
+  float prev[ACC ? RH : 1];
+  if constexpr (ACC) {
+#pragma unroll
+    for (int r = 0; r < RH; ++r) prev[r] = ((const float*)out)[min(row0 + r, N - 1)];
+  }
   // Keep the issue order: staging loads, then weight loads, then LDS writes (which
   // then wait only for the older staging loads).
   __builtin_amdgcn_sched_barrier(0);
@@ -209,7 +220,12 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     for (int r = 0; r < R; ++r) {
       float v = wave_sum_to_lane63(acc[r]);
       if (SRC == SRC_PLAIN && pa.row_scale) v *= rsc;
-      if (lane == 63 && row0 + r < N) store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+      if (lane == 63 && row0 + r < N) {
+        if constexpr (ACC)
+          ((float*)out)[row0 + r] = prev[r] + v;
+        else
+          store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+      }
     }
   }
 }
