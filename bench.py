@@ -552,8 +552,9 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
            "GBs": round((wb + kvb) / (ms * 1e-3) / 1e9, 1),
            "frac_hbm_peak": round((wb + kvb) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            # per layer: Q/K/V (norm fused), attention, o_proj, gate/up (norm + SwiGLU fused),
-           # down; head: final norm, lm_head, argmax partials, argmax + next embedding
-           "launches_per_token": 5 * s.layers + 4,
+           # down; head: final norm, lm_head (a W4A8 one leaves the argmax candidates, a
+           # W4A16 one is followed by an argmax-partials launch), argmax + next embedding
+           "launches_per_token": 5 * s.layers + (3 if m.lm_head_w4a8 else 4),
            "attn_key_split": attn_key_split(s, max_seq)}
     log(f"decode 3B: {ms * 1e3:.1f} us/token, {tok_s:.1f} tok/s, {rec['GBs']} GB/s")
     if not no_cpu:

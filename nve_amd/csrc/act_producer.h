@@ -227,7 +227,7 @@ __device__ __forceinline__ uint4 prod_bf16x8(const float (&v)[8]) {
 
 namespace nve {
 
-// ---- paired-row epilogues of the fused GEMV launches ----------------------------------
+// ---- epilogues of the fused GEMV launches (paired rows, or the greedy candidate) ------
 // PAIR_SWIGLU: a wave computes R/2 rows of gate (segment 0) and the same rows of up (the
 //   matrix in nib[1] / sc[1]) and writes silu(gate) * up (src/ops.rs:62-64).
 // PAIR_ROPE: the Q/K/V launch of a decode layer.  A wave computes, for R/2 pairs p of a
@@ -235,9 +235,12 @@ namespace nve {
 //   RoPE pair (src/ops.rs:264-276) and finishes the attention's input in its epilogue:
 //   q rotated and multiplied by qscale (f32), the new key rotated and the new value, both
 //   rounded to bf16, written straight into the KV cache at the token's position.
-enum { PAIR_NONE = 0, PAIR_SWIGLU = 1, PAIR_ROPE = 2 };
+// PAIR_ARGMAX: plain rows, stored as usual, and each workgroup's greedy candidate
+// (largest value, lowest index among equal ones, NaN never) written to
+// arg_v / arg_i[workgroup].
+enum { PAIR_NONE = 0, PAIR_SWIGLU = 1, PAIR_ROPE = 2, PAIR_ARGMAX = 3 };
 
-struct RopeArgs {
+struct EpiArgs {
   float* q;            // f32 [num_heads * D]
   uint16_t* kc;        // bf16 [num_kv_heads, max_seq, D]
   uint16_t* vc;
@@ -246,16 +249,18 @@ struct RopeArgs {
   const float* sin;
   int max_seq, half;   // half = D / 2
   float qscale;
+  float* arg_v;        // PAIR_ARGMAX: per-workgroup candidates
+  int* arg_i;
 };
 
 __host__ __device__ __forceinline__ int rope_row(int p, int half, bool second) {
   return (p / half) * 2 * half + p % half + (second ? half : 0);
 }
 
-__device__ __forceinline__ int rope_pos(const RopeArgs& ra) { return min(max(*ra.pos, 0), ra.max_seq - 1); }
+__device__ __forceinline__ int rope_pos(const EpiArgs& ra) { return min(max(*ra.pos, 0), ra.max_seq - 1); }
 
 // Segment sg of the Q/K/V launch: 0 = q, 1 = k, 2 = v; x0 / x1 = rows d / d + half.
-__device__ __forceinline__ void rope_store(const RopeArgs& ra, int sg, int p, float x0, float x1, float c, float s,
+__device__ __forceinline__ void rope_store(const EpiArgs& ra, int sg, int p, float x0, float x1, float c, float s,
                                            int pos) {
   const int half = ra.half, head = p / half, d = p % half;
   if (sg == 0) {

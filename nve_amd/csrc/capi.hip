@@ -192,7 +192,7 @@ int nve_hip_grouped_matvec_w4a8_x(const void* x, int x_dtype, const nve_w4_mat* 
   if (K > 16384) return set_status(NVE_ERR_TOO_LARGE);
   if (!aligned(x, 16)) return set_status(NVE_ERR_ALIGN);
   return from_hip(launch_w4a8_fused(src_of(x_dtype), nve::PAIR_NONE, nve::ProdArgs{x, nullptr, 0.0f}, s, out_dtype, K,
-                                    (hipStream_t)stream, nve::RopeArgs{}));
+                                    (hipStream_t)stream, nve::EpiArgs{}));
 }
 
 int nve_hip_matvec_w4a8_x(const void* x, int x_dtype, const uint8_t* nibbles, const float* wt_scales, void* out,

@@ -454,12 +454,13 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
 }
 
 // ---- head: greedy argmax (first maximum), next-token embedding, position advance --
-// Two launches: kArgmaxBlocks workgroups each reduce a slice of the logits to (value,
-// index); one workgroup then reduces the partials, writes the token, embeds its row
-// into hidden and advances the position (the launch boundary orders the partials'
-// writes before their reads -- no device-scope fence or arrival counter).  NaN never
-// wins; among equal values the lowest index wins (src/ops.rs:485-495 keeps the first
-// maximum).
+// The W4A8 lm_head launch leaves one (value, index) candidate per workgroup (its
+// PAIR_ARGMAX epilogue); after a W4A16 lm_head, kArgmaxBlocks workgroups each reduce a
+// slice of the logits to one.  One workgroup then reduces the candidates, writes the
+// token, embeds its row into hidden and advances the position (the launch boundary
+// orders the candidates' writes before their reads -- no device-scope fence or arrival
+// counter).  NaN never wins; among equal values the lowest index wins
+// (src/ops.rs:485-495 keeps the first maximum).
 constexpr int kArgmaxBlocks = 128;
 
 __device__ __forceinline__ void argmax_merge(float& b, int& bi, float o, int oi) {
@@ -487,6 +488,7 @@ __device__ __forceinline__ void argmax_xor(float& b, int& bi) {
   argmax_merge(b, bi, __builtin_bit_cast(float, (uint32_t)r[1]), (int)ri[1]);
 }
 
+template <int NW>
 __device__ __forceinline__ void argmax_block(float& best, int& bi, float* s_v, int* s_i) {
   argmax_dpp<0xB1>(best, bi);   // quad_perm [1,0,3,2]
   argmax_dpp<0x4E>(best, bi);   // quad_perm [2,3,0,1]
@@ -500,7 +502,7 @@ __device__ __forceinline__ void argmax_block(float& best, int& bi, float* s_v, i
   }
   __syncthreads();
   if (threadIdx.x == 0)
-    for (int w = 1; w < 4; ++w) argmax_merge(best, bi, s_v[w], s_i[w]);
+    for (int w = 1; w < NW; ++w) argmax_merge(best, bi, s_v[w], s_i[w]);
 }
 
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits, int V,
@@ -538,28 +540,40 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
   } else {
     for (int i = lo + threadIdx.x; i < hi; i += 256) argmax_merge(best, bi, logits[i], i);
   }
-  argmax_block(best, bi, s_v, s_i);
+  argmax_block<4>(best, bi, s_v, s_i);
   if (threadIdx.x == 0) {
     part_v[blockIdx.x] = best;
     part_i[blockIdx.x] = bi;
   }
 }
 
-__global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restrict__ part_v,
-                                                           const int* __restrict__ part_i,
-                                                           const uint16_t* __restrict__ embed, int H,
-                                                           float* __restrict__ hidden, int* __restrict__ token_out,
-                                                           int* __restrict__ d_pos) {
-  __shared__ float s_v[4];
-  __shared__ int s_i[4];
+// nparts candidates (the argmax_partial_kernel slices, or the per-workgroup candidates
+// of the lm_head GEMV's PAIR_ARGMAX epilogue), merged by 1024 threads: every thread's
+// loads are issued before any is merged.
+__global__ __launch_bounds__(1024) void argmax_embed_kernel(const float* __restrict__ part_v,
+                                                            const int* __restrict__ part_i, int nparts,
+                                                            const uint16_t* __restrict__ embed, int H,
+                                                            float* __restrict__ hidden, int* __restrict__ token_out,
+                                                            int* __restrict__ d_pos) {
+  __shared__ float s_v[16];
+  __shared__ int s_i[16];
   __shared__ int s_tok;
   float best = -INFINITY;
   int bi = 0x7fffffff;
-  if (threadIdx.x < kArgmaxBlocks) {
-    best = part_v[threadIdx.x];
-    bi = part_i[threadIdx.x];
+  constexpr int U = 8;
+  for (int base = 0; base < nparts; base += 1024 * U) {
+    float v[U];
+    int ix[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + 1024 * u + (int)threadIdx.x;
+      v[u] = i < nparts ? part_v[i] : -INFINITY;
+      ix[u] = i < nparts ? part_i[i] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) argmax_merge(best, bi, v[u], ix[u]);
   }
-  argmax_block(best, bi, s_v, s_i);
+  argmax_block<16>(best, bi, s_v, s_i);
   if (threadIdx.x == 0) {
     if (bi == 0x7fffffff) bi = 0;  // all NaN / -inf: token 0
     s_tok = bi;
@@ -567,7 +581,7 @@ __global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restri
   }
   __syncthreads();
   const int tok = s_tok;
-  for (int i = threadIdx.x; i < H; i += 256) hidden[i] = bf16_bits_to_f32(embed[(size_t)tok * H + i]);
+  for (int i = threadIdx.x; i < H; i += 1024) hidden[i] = bf16_bits_to_f32(embed[(size_t)tok * H + i]);
   if (threadIdx.x == 0) *d_pos += 1;
 }
 
@@ -593,8 +607,8 @@ struct DecodeWs {
   float* v;            // [Hkv*D]
   float* gate;         // [F]
   float* up;           // [F]
-  float* arg_v;        // [kArgmaxBlocks]
-  int* arg_i;          // [kArgmaxBlocks]
+  float* arg_v;        // [argmax_slots]: greedy candidates of the head
+  int* arg_i;          // [argmax_slots]
   float* logits;       // [V] (head only, when the caller passes no logits buffer)
   float* part;         // [kMaxAttnSplit][Hq][D + 4] key-split attention partials
   float* hmid;         // [H] residual after the attention sub-layer (one-kernel layer)
@@ -611,6 +625,13 @@ constexpr int kAttnSplit8Slots = 1024;
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 
+
+// Candidate slots of the greedy head: the lm_head GEMV writes one per workgroup, at
+// least four rows each.
+static int argmax_slots(const nve_decode_config& c) {
+  const int per_wg = ((c.vocab > 0 ? c.vocab : 1) + 3) / 4;
+  return per_wg > nve::kArgmaxBlocks ? per_wg : nve::kArgmaxBlocks;
+}
 
 static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
   DecodeWs w{};
@@ -633,8 +654,8 @@ static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
   w.v = (float*)take(kd * 4);
   w.gate = (float*)take((size_t)c.ffn * 4);
   w.up = (float*)take((size_t)c.ffn * 4);
-  w.arg_v = (float*)take(nve::kArgmaxBlocks * 4);
-  w.arg_i = (int*)take(nve::kArgmaxBlocks * 4);
+  w.arg_v = (float*)take((size_t)argmax_slots(c) * 4);
+  w.arg_i = (int*)take((size_t)argmax_slots(c) * 4);
   w.logits = (float*)take((size_t)(c.vocab > 0 ? c.vocab : 1) * 4);
   w.part = (float*)take((size_t)kMaxAttnSplit * c.num_heads * (c.head_dim + 4) * 4);
   w.hmid = (float*)take((size_t)c.hidden * 4);
@@ -763,7 +784,7 @@ static hipError_t gemv(bool w4a8, const DecodeWs& ws, const W4Segs& sg, int out_
 }
 
 static hipError_t gemv_fused(bool w4a8, int src, int pair, const nve::ProdArgs& pa, const W4Segs& sg, int out_dt,
-                             int K, hipStream_t s, const nve::RopeArgs& ra = nve::RopeArgs{}) {
+                             int K, hipStream_t s, const nve::EpiArgs& ra = nve::EpiArgs{}) {
   return w4a8 ? launch_w4a8_fused(src, pair, pa, sg, out_dt, K, s, ra)
               : launch_w4a16_fused(src, pair, pa, sg, out_dt, K, s, ra);
 }
@@ -833,7 +854,7 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
     const W4Segs sg = segs3(qkv, outs, 3);
     if (fuse) {
       // RoPE and the KV-cache append run in the epilogue (PAIR_ROPE)
-      const nve::RopeArgs ra{ws.q, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.max_seq,
+      const nve::EpiArgs ra{ws.q, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.max_seq,
                              c.head_dim / 2, 1.4426950408889634f / sqrtf((float)c.head_dim)};
       NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_ROPE, nve::ProdArgs{io.hidden, w.input_norm, c.eps}, sg,
                          NVE_DT_F32, H, s, ra));
@@ -891,17 +912,23 @@ int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8
   float* logits = hd.logits ? hd.logits : ws.logits;
   // (the RMSNorm stays a kernel of its own here: fused into the lm_head staging it
   // would be recomputed by every one of the ~8000 workgroups, measured 44 us vs 42)
-  if (w4a8) {
-    NVE_TRY(launch_rmsnorm(c, hd.hidden, hd.final_norm, w4a8, ws, s));
-    NVE_TRY(launch_w4a8(ws.xq, ws.xs, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
+  int ncand = nve::kArgmaxBlocks;
+  NVE_TRY(launch_rmsnorm(c, hd.hidden, hd.final_norm, w4a8, ws, s));
+  if (w4a8 && (hd.lm_head.n + 3) / 4 <= argmax_slots(c)) {
+    // the lm_head launch leaves one greedy candidate per workgroup (of >= 4 rows)
+    NVE_TRY(launch_w4a8_argmax(ws.xq, ws.xs, one_seg(hd.lm_head, logits), c.hidden, ws.arg_v, ws.arg_i, &ncand, s));
   } else {
-    NVE_TRY(launch_rmsnorm(c, hd.hidden, hd.final_norm, w4a8, ws, s));
-    NVE_TRY(launch_w4a16(ws.act16, NVE_DT_F16, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
+    // (also a W4A8 lm_head with more rows than the workspace's vocab has slots for,
+    // possible when the caller passes its own logits buffer)
+    if (w4a8)
+      NVE_TRY(launch_w4a8(ws.xq, ws.xs, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
+    else
+      NVE_TRY(launch_w4a16(ws.act16, NVE_DT_F16, one_seg(hd.lm_head, logits), NVE_DT_F32, c.hidden, s));
+    hipLaunchKernelGGL(nve::argmax_partial_kernel, dim3(nve::kArgmaxBlocks), dim3(256), 0, s, logits, hd.lm_head.n,
+                       ws.arg_v, ws.arg_i);
   }
-  hipLaunchKernelGGL(nve::argmax_partial_kernel, dim3(nve::kArgmaxBlocks), dim3(256), 0, s, logits, hd.lm_head.n,
-                     ws.arg_v, ws.arg_i);
-  hipLaunchKernelGGL(nve::argmax_embed_kernel, dim3(1), dim3(256), 0, s, ws.arg_v, ws.arg_i, hd.embed, c.hidden,
-                     hd.hidden, hd.token_out, hd.pos);
+  hipLaunchKernelGGL(nve::argmax_embed_kernel, dim3(1), dim3(1024), 0, s, ws.arg_v, ws.arg_i, ncand, hd.embed,
+                     c.hidden, hd.hidden, hd.token_out, hd.pos);
   return (int)hipGetLastError();
 }
 

@@ -45,7 +45,7 @@ namespace nve {
 // computes both rows of R/2 RoPE pairs and writes the attention's input (rope_store).
 template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, int PAIR = PAIR_NONE>
 __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict__ x, W4Segs segs,
-                                                         int K, ProdArgs pa, RopeArgs ra) {
+                                                         int K, ProdArgs pa, EpiArgs ra) {
   constexpr bool SWI = PAIR == PAIR_SWIGLU, ROPE = PAIR == PAIR_ROPE;
   static_assert(SRC == SRC_PLAIN || (!MULTI && MODE == MODE_F16), "fused producers: one-pass fp16 staging");
   static_assert(PAIR == PAIR_NONE || (R % 2 == 0 && !MULTI && MODE != MODE_F32), "paired rows: even R, one pass");
@@ -258,7 +258,7 @@ namespace nve_host {
 template <int MODE, int XDT, int OUT_DT, int R, int NJ, bool MULTI, int SRC = nve::SRC_PLAIN,
           int PAIR = nve::PAIR_NONE>
 static hipError_t launch_w4a16_t(const void* x, const W4Segs& segs, int K, hipStream_t stream,
-                                 const nve::ProdArgs& pa = nve::ProdArgs{}, const nve::RopeArgs& ra = nve::RopeArgs{}) {
+                                 const nve::ProdArgs& pa = nve::ProdArgs{}, const nve::EpiArgs& ra = nve::EpiArgs{}) {
   const size_t lds = nve::w4a16_lds_bytes(MODE, K) + (SRC == nve::SRC_NORM ? 64 : 0);
   auto kern = nve::w4a16_gemv_kernel<MODE, XDT, OUT_DT, R, NJ, MULTI, SRC, PAIR>;
   if (lds > 65536) {
@@ -283,7 +283,7 @@ static hipError_t launch_w4a16_m(const void* x, W4Segs segs, int K, hipStream_t 
 
 template <int OUT_DT, int SRC, int PAIR>
 static hipError_t launch_w4a16_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream,
-                                       const nve::RopeArgs& ra) {
+                                       const nve::EpiArgs& ra) {
   const W4Tiling t = nve::attn_splits_of(SRC) ? choose_merge_tiling(segs, K) : choose_w4_tiling(segs, K);
   if (t.multi) return hipErrorInvalidValue;
   if (PAIR != nve::PAIR_NONE) {
@@ -342,7 +342,7 @@ hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt,
 //   NORM, F16, swiglu  gate/up -> silu(gate) * up rounded to fp16 (the down input);
 //   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
 hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                              hipStream_t stream, const nve::RopeArgs& ra) {
+                              hipStream_t stream, const nve::EpiArgs& ra) {
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && pair == nve::PAIR_ROPE)
     return launch_w4a16_fused_t<NVE_DT_F32, nve::SRC_NORM, nve::PAIR_ROPE>(pa, segs, K, stream, ra);
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32 && pair == nve::PAIR_NONE)

@@ -43,11 +43,12 @@ namespace nve {
 template <int OUT_DT, int R, int NJ, bool MULTI, int SRC = SRC_PLAIN, int PAIR = PAIR_NONE>
 __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xs,
-                                                        W4Segs segs, int K, ProdArgs pa, RopeArgs ra) {
-  constexpr bool SWI = PAIR == PAIR_SWIGLU, ROPE = PAIR == PAIR_ROPE;
+                                                        W4Segs segs, int K, ProdArgs pa, EpiArgs ra) {
+  constexpr bool SWI = PAIR == PAIR_SWIGLU, ROPE = PAIR == PAIR_ROPE, PAIRED = SWI || ROPE;
   static_assert(SRC == SRC_PLAIN || !MULTI, "fused producers stage in one pass");
-  static_assert(PAIR == PAIR_NONE || (R % 2 == 0 && !MULTI), "paired rows: even R, one pass");
-  constexpr int RH = PAIR != PAIR_NONE ? R / 2 : R;  // output rows (pairs) per wave
+  static_assert(!PAIRED || (R % 2 == 0 && !MULTI), "paired rows: even R, one pass");
+  static_assert(PAIR != PAIR_ARGMAX || OUT_DT == NVE_DT_F32, "greedy candidates over f32 logits");
+  constexpr int RH = PAIRED ? R / 2 : R;  // output rows (pairs) per wave
   constexpr int SPT = (NJ + 1) / 2;  // staging passes: 2*nb <= 128*NJ chunks of 16 B
   extern __shared__ int4 lds[];
   const int nb = K >> 5;
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   auto issue = [&](int jb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int rr = min(row0 + (PAIR != PAIR_NONE ? r % RH : r), N - 1);
+      const int rr = min(row0 + (PAIRED ? r % RH : r), N - 1);
       const int row = ROPE ? rope_row(rr, ra.half, r >= RH) : rr;
       const uint8_t* mn = (SWI && r >= RH) ? segs.nib[1] : nib;
       const float* ms = (SWI && r >= RH) ? segs.sc[1] : ws;
@@ -216,6 +217,8 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     }
   } else {
     const float rsc = (SRC == SRC_PLAIN && pa.row_scale) ? bf16_bits_to_f32(*pa.row_scale) : 1.0f;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float v = wave_sum_to_lane63(acc[r]);
@@ -225,6 +228,24 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
           ((float*)out)[row0 + r] = prev[r] + v;
         else
           store_out<OUT_DT>(out, (size_t)(row0 + r), v);
+        // the merge rule of the greedy head: larger value, or the lower index of equal
+        // ones (-inf included); NaN never wins
+        if (PAIR == PAIR_ARGMAX && (v > best || (v == best && row0 + r < bi))) best = v, bi = row0 + r;
+      }
+    }
+    if constexpr (PAIR == PAIR_ARGMAX) {
+      // the workgroup's candidate: lane 63 of each wave holds its rows' candidate
+      __shared__ float s_av[4];
+      __shared__ int s_ai[4];
+      if (lane == 63) s_av[wave] = best, s_ai[wave] = bi;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        best = s_av[0];
+        bi = s_ai[0];
+        for (int w = 1; w < 4; ++w)
+          if (s_av[w] > best || (s_av[w] == best && s_ai[w] < bi)) best = s_av[w], bi = s_ai[w];
+        ra.arg_v[wg - wg0] = best;
+        ra.arg_i[wg - wg0] = bi;
       }
     }
   }
@@ -257,7 +278,7 @@ namespace nve_host {
 template <int OUT_DT, int R, int NJ, bool MULTI, int SRC, int PAIR>
 static hipError_t launch_w4a8_t(const int8_t* xq, const float* xs, const W4Segs& segs, int K,
                                 int grid, const nve::ProdArgs& pa, hipStream_t stream,
-                                const nve::RopeArgs& ra = nve::RopeArgs{}) {
+                                const nve::EpiArgs& ra = nve::EpiArgs{}) {
   const size_t lds = nve::w4a8_lds_bytes(K) + (SRC == nve::SRC_NORM ? 64 : 0);
   auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI, SRC, PAIR>;
   if (lds > 65536) {
@@ -285,7 +306,7 @@ static hipError_t launch_w4a8_dt(const int8_t* xq, const float* xs, W4Segs segs,
 // Fused-producer launches (one-shot kernels, one staging pass: K <= 16384).
 template <int OUT_DT, int SRC, int PAIR>
 static hipError_t launch_w4a8_fused_t(const nve::ProdArgs& pa, W4Segs segs, int K, hipStream_t stream,
-                                      const nve::RopeArgs& ra) {
+                                      const nve::EpiArgs& ra) {
   const W4Tiling t = nve::attn_splits_of(SRC) ? choose_merge_tiling(segs, K) : choose_w4_tiling(segs, K);
   if (t.multi) return hipErrorInvalidValue;
   if (PAIR != nve::PAIR_NONE) {
@@ -336,6 +357,25 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
   }
 }
 
+hipError_t launch_w4a8_argmax(const int8_t* xq, const float* xs, const W4Segs& segs_in, int K, float* arg_v,
+                              int* arg_i, int* ncand, hipStream_t stream) {
+  W4Segs segs = segs_in;
+  if (segs.nseg != 1) return hipErrorInvalidValue;
+  const W4Tiling t = choose_w4_tiling(segs, K);
+  finalize_segments(segs, t.R);
+  *ncand = segs.wg_total;
+  nve::EpiArgs ra{};
+  ra.arg_v = arg_v;
+  ra.arg_i = arg_i;
+#define NVE_W4A8_ARG_CASE(RR, JJ, MM)            \
+  if (t.R == RR && t.NJ == JJ && t.multi == MM) \
+    return launch_w4a8_t<NVE_DT_F32, RR, JJ, MM, nve::SRC_PLAIN, nve::PAIR_ARGMAX>(xq, xs, segs, K, segs.wg_total, \
+                                                                                  nve::ProdArgs{}, stream, ra);
+  NVE_W4_TILING_CASES(NVE_W4A8_ARG_CASE)
+#undef NVE_W4A8_ARG_CASE
+  return hipErrorInvalidValue;
+}
+
 // Decode-layer W4A8 GEMVs with a fused producer (act_producer.h):
 //   NORM, F32, rope    Q/K/V from the residual and the norm weights, RoPE + KV append
 //                      in the epilogue (PAIR_ROPE; out[] unused);
@@ -344,7 +384,7 @@ hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, in
 //   F32, F32_ACCUM     down from that f32 vector, quantized in the staging;
 //   ATTN2/4, F32_ACCUM o_proj from the key-split attention partials.
 hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                             hipStream_t stream, const nve::RopeArgs& ra) {
+                             hipStream_t stream, const nve::EpiArgs& ra) {
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F16 && pair == nve::PAIR_SWIGLU)
     return launch_w4a8_fused_t<NVE_DT_F16, nve::SRC_NORM, nve::PAIR_SWIGLU>(pa, segs, K, stream, ra);
   if (src == nve::SRC_NORM && out_dt == NVE_DT_F32) {

@@ -190,19 +190,23 @@ int layer_forward_decode_noalloc(const nve_decode_config& c, const nve_layer_wei
 }  // namespace nve_host
 namespace nve {
 struct ProdArgs;
-struct RopeArgs;
+struct EpiArgs;
 }
 namespace nve_host {
 // pair: nve::PAIR_NONE / PAIR_SWIGLU / PAIR_ROPE (act_producer.h); ra is read by PAIR_ROPE only.
 hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                             hipStream_t stream, const nve::RopeArgs& ra);
+                             hipStream_t stream, const nve::EpiArgs& ra);
 hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
-                              hipStream_t stream, const nve::RopeArgs& ra);
+                              hipStream_t stream, const nve::EpiArgs& ra);
 hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);
 hipError_t launch_w4a8_rowscale(const int8_t* xq, const uint16_t* row_scale, const W4Segs& segs, int out_dt, int K,
                                 hipStream_t stream);
+// One-shot W4A8 GEMV to f32 logits that also writes each workgroup's greedy candidate
+// (PAIR_ARGMAX) to arg_v / arg_i; *ncand = the number of workgroups (<= ceil(N / 4)).
+hipError_t launch_w4a8_argmax(const int8_t* xq, const float* xs, const W4Segs& segs, int K, float* arg_v,
+                              int* arg_i, int* ncand, hipStream_t stream);
 hipError_t launch_w4a8_block_acc(const int8_t* xq, const uint8_t* nib, int32_t* acc, int N, int K,
                                  hipStream_t stream);
 hipError_t launch_w4a16(const void* x, int x_dt, const W4Segs& segs, int out_dt, int K,
