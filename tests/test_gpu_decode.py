@@ -362,3 +362,40 @@ def test_head_argmax_ties_nan_and_slices(torch_dev, lm8):
     sc.view(vocab, nb)[r0] = float("nan")
     tok, lg = run()
     assert tok == (copies[0] if lg[copies[0]] > 0 else 0), tok
+
+
+@pytest.mark.parametrize("lm8", [True, False])
+def test_head_with_caller_logits_and_more_rows_than_vocab(torch_dev, lm8):
+    """A caller that passes its own logits buffer may hand the head an lm_head with more
+    rows than the config's vocabulary (nve_decode_head): the W4A8 head then has more
+    workgroups than the workspace has greedy-candidate slots and takes the launch over
+    the logits instead.  Extra rows that copy rows 0..39 tie with them, so the token is
+    the same as with the plain lm_head (the first maximum) and the copied logits equal
+    the originals."""
+    torch = torch_dev
+    import ctypes as C
+    from nve_amd._lib import DecodeHead, W4Weight, check, lib
+    vocab, extra = 512, 40
+    m = _model(torch, 4, 2, 64, layers=1, vocab=vocab, lm_head_w4a8=lm8, prefill=4, max_seq=16)
+    nib, sc = m.lm_head
+    H = m.shape.hidden
+    nib2 = torch.cat([nib.view(vocab, -1), nib.view(vocab, -1)[:extra]]).contiguous()
+    sc2 = torch.cat([sc.view(vocab, -1), sc.view(vocab, -1)[:extra]]).contiguous()
+    logits2 = torch.full((vocab + extra,), float("nan"), dtype=torch.float32, device="cuda")
+    tok2 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for step in range(3):
+        m.start(3 + step)
+        m.head()
+        torch.cuda.synchronize()
+        tok, lg = int(m.token.item()), m.logits.cpu().numpy()
+        m.start(3 + step)
+        hd = DecodeHead(m.hidden.data_ptr(), m.final_norm.data_ptr(),
+                        W4Weight(nib2.data_ptr(), sc2.data_ptr(), vocab + extra, H), m.embed.data_ptr(),
+                        logits2.data_ptr(), tok2.data_ptr(), m.pos.data_ptr(), m.workspace.data_ptr())
+        check("nve_hip_decode_head",
+              lib().nve_hip_decode_head(C.byref(m.cfg), C.byref(hd), int(lm8), torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        lg2 = logits2.cpu().numpy()
+        print(f"lm8={lm8} step {step}: token {tok} / {int(tok2.item())}", flush=True)
+        assert np.array_equal(lg2[:vocab], lg) and np.array_equal(lg2[vocab:], lg[:extra])
+        assert int(tok2.item()) == tok
