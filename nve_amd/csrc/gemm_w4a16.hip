@@ -21,6 +21,7 @@
 // weight-streaming kernel (gemm_w4a16_small_kernel below).
 
 #include "common.h"
+#include "lds_ring.h"
 #include "w4_launch.h"
 
 namespace nve {
@@ -381,6 +382,184 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
   }
 }
 
+// ---- small M (M <= 16), K % 128 == 0, no AWQ: the LDS-ring form ----------------------
+// The weight-streaming kernel above with the W4A8 batched kernel's LDS ring
+// (gemv_w4a8_batched.hip) in place of its VGPR loads and ds_bpermute moves: every load
+// is a global -> LDS transfer into a per-wave slot holding one K quad --
+//   W  T x 1 KiB   weight tile t, 16 rows x 64 B (4 lanes per row), pieces swizzled as
+//                  in the W4A8 ring (load lane (row a, slot s) fetches piece (s - a/2) & 3)
+//   SC T x 256 B   the tile's 16 x 4 block scales
+//   A  EU x 1 KiB  activation rows 4a..4a+3 of the quad, 256 B each (4 blocks of 32
+//                  fp16 / bf16), the 16-byte pieces of row r stored at piece ^ (r & 15)
+//                  so that the 16 rows' reads of one k-set fall on different banks
+// -- and the operand lanes read the slot: the weight piece (ds_read_b128 and the 4x4
+// permlane transpose: nibble dword g of the 4 blocks), the row's scales, and per block
+// the two 8-byte k-runs {4g..4g+3} and {16+4g..16+4g+3} of the activation row.  The
+// nibbles are extracted low / high per byte, which yields that same k order, so the B
+// operand (the reference dequant f16/bf16(fma(n, s, -8 s)), as above) needs no permute.
+// One quad in flight per wave, 16 waves; workgroups take ceil(N / 256) rows each (one
+// per CU), the last tile partly masked (masked lanes issue no transfers; lane 0 always
+// does, so every wave instruction counts once and the vmcnt waits are exact).
+template <int T, int EU>
+struct W16Ring {
+  static constexpr int W = 0, SC = T * 1024, A = SC + T * 256, SLOT = A + EU * 1024;
+  static constexpr int LOADS = 2 * T + EU;
+};
+
+template <bool BF16, int OUT_DT, int T, int EU>
+__global__ __launch_bounds__(1024) void gemm_w4a16_ring_kernel(const uint16_t* __restrict__ x,
+                                                               const uint8_t* __restrict__ nib,
+                                                               const float* __restrict__ ws,
+                                                               void* __restrict__ out, int M, int N, int K,
+                                                               int rows_per_wg) {
+  constexpr int KS = 16;
+  using L = W16Ring<T, EU>;
+  constexpr int kRing = KS * L::SLOT;
+  constexpr int kRed = KS * T * 16 * (4 * EU + 1) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kRing > kRed ? kRing : kRed];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nl = lane & 15, g = lane >> 4;  // operand layout
+  const int lr = lane >> 2, lp = lane & 3;  // weight load layout
+  const int row0 = blockIdx.x * rows_per_wg;
+  const int nb = K >> 5, nq = nb >> 2;
+  const int nqw = (nq + KS - 1) / KS;
+  char* const ring = smem + wave * L::SLOT;
+
+  const uint8_t* wsrc[T];
+  const float* ssrc[T];
+  bool wok[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int rr = 16 * t + lr;
+    const int r = min(row0 + rr, N - 1);
+    wok[t] = (rr < rows_per_wg && row0 + rr < N) || lane == 0;
+    wsrc[t] = nib + (size_t)r * (K >> 1) + 16 * ((lp - (lr >> 1)) & 3);
+    ssrc[t] = ws + (size_t)r * nb + lp;
+  }
+  // activation transfer a: lane l -> row 4a + l / 16, stored piece l % 16 = source piece ^ row
+  const char* asrc[EU];
+  bool aok[EU];
+#pragma unroll
+  for (int a = 0; a < EU; ++a) {
+    const int m = 4 * a + (lane >> 4);
+    aok[a] = m < M || lane == 0;
+    asrc[a] = (const char*)(x + (size_t)min(m, M - 1) * K) + 16 * ((lane & 15) ^ (m & 15));
+  }
+  auto issue = [&](int i) {
+    const int q = min(wave + KS * i, nq - 1);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (wok[t]) lds_dma16(wsrc[t] + 64 * q, ring + L::W + t * 1024);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if (wok[t]) lds_dma4(ssrc[t] + 4 * q, ring + L::SC + t * 256);
+#pragma unroll
+    for (int a = 0; a < EU; ++a)
+      if (aok[a]) lds_dma16(asrc[a] + 256 * q, ring + L::A + a * 1024);
+  };
+
+  // A row nl holds activation row am (rows >= M read row M - 1, never stored)
+  const int am = 4 * (nl & 3) + (nl >> 2);
+  const int ar = min(am, M - 1);
+  const uint32_t rd_w = 16 * (4 * nl + ((g + (nl >> 1)) & 3));
+  uint32_t rd_lo[4], rd_hi[4];
+  {
+    const uint32_t rb = L::A + (ar >> 2) * 1024 + (ar & 3) * 256 + 8 * (g & 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rd_lo[j] = rb + 16 * ((4 * j + (g >> 1)) ^ (ar & 15));
+      rd_hi[j] = rb + 16 * ((4 * j + 2 + (g >> 1)) ^ (ar & 15));
+    }
+  }
+  f4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](int i) {
+    if (wave + KS * i >= nq) return;  // clamped duplicate quad (wave-uniform)
+    const uint32_t sb = lds_addr(ring);
+    u32x2_t xl[4], xh[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xl[j] = ds_read64(sb + rd_lo[j]);
+      xh[j] = ds_read64(sb + rd_hi[j]);
+    }
+    u32x4_t wr[T], sr[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      wr[t] = ds_read128(sb + L::W + t * 1024 + rd_w);
+      sr[t] = ds_read128(sb + L::SC + t * 256 + nl * 16);
+    }
+    lgkm_wait();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      tie(xl[j]);
+      tie(xh[j]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      tie(wr[t]);
+      tie(sr[t]);
+    }
+    uint4 a[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = make_uint4(xl[j].x, xl[j].y, xh[j].x, xh[j].y);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint32_t c0 = wr[t].x, c1 = wr[t].y, c2 = wr[t].z, c3 = wr[t].w;
+      transpose4(c0, c1, c2, c3);  // lane (n, g): nibble dword g of blocks 4q+0..3
+      const uint32_t cj[4] = {c0, c1, c2, c3};
+      const float scj[4] = {__uint_as_float(sr[t].x), __uint_as_float(sr[t].y), __uint_as_float(sr[t].z),
+                            __uint_as_float(sr[t].w)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float s = scj[j], s8 = -8.0f * s;
+        const uint32_t lo = cj[j] & 0x0F0F0F0Fu, hi = (cj[j] >> 4) & 0x0F0F0F0Fu;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = fmaf((float)((lo >> (8 * e)) & 0xffu), s, s8);
+          v[4 + e] = fmaf((float)((hi >> (8 * e)) & 0xffu), s, s8);
+        }
+        const uint4 b = make_uint4(cvt_pk<BF16>(v[0], v[1]), cvt_pk<BF16>(v[2], v[3]), cvt_pk<BF16>(v[4], v[5]),
+                                   cvt_pk<BF16>(v[6], v[7]));
+        acc[t] = mfma16<BF16>(a[j], b, acc[t]);
+      }
+    }
+  };
+
+  issue(0);
+  int i = 0;
+  for (; i + 1 < nqw; ++i) {
+    wait_vmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(i + 1);
+  }
+  wait_vmcnt<0>();
+  __builtin_amdgcn_sched_barrier(0);
+  compute(i);
+
+  __syncthreads();  // every wave is done with its slot: reuse the LDS for the reduction
+  float(*s_red)[T * 16][4 * EU + 1] = (float(*)[T * 16][4 * EU + 1])smem;
+  // D layout: lane (n, g) holds rows i = 4g + e (activation row 4e + g) of column n
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < EU; ++e) s_red[wave][16 * t + nl][4 * e + g] = acc[t][e];
+  __syncthreads();
+  const int rows = min(rows_per_wg, N - row0);
+  for (int xi = threadIdx.x; xi < T * 16 * 4 * EU; xi += 64 * KS) {
+    const int mm = xi / (16 * T), r = xi % (16 * T);
+    float y = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < KS; ++w2) y += s_red[w2][r][mm];
+    if (mm < M && r < rows) store_out<OUT_DT>(out, (size_t)mm * N + row0 + r, y);
+  }
+}
+
 // out[i] = sum over z = 0 .. split-1 of part[z * n + i], in that order.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            size_t n, int split) {
@@ -485,9 +664,47 @@ static hipError_t launch_small_o(const void* x, int M, const uint8_t* nib, const
   return hipGetLastError();
 }
 
+// M <= 16 without AWQ, K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
+// rows per workgroup (16 below 4096 rows), one activation transfer per 4 rows of M.
+template <bool BF16, int OUT_DT, int T>
+static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
+                                int rpw, hipStream_t s) {
+  const dim3 grid((N + rpw - 1) / rpw);
+#define NVE_R16(EU) \
+  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, OUT_DT, T, EU>), grid, dim3(1024), 0, s, (const uint16_t*)x, \
+                     nib, sc, out, M, N, K, rpw)
+  if (M <= 4) NVE_R16(1);
+  else if (M <= 8) NVE_R16(2);
+  else NVE_R16(4);
+#undef NVE_R16
+  return hipGetLastError();
+}
+
+template <bool BF16, int OUT_DT>
+static hipError_t launch_ring_o(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
+                                hipStream_t s) {
+  const int rpw = N <= 4096 ? 16 : (N + 255) / 256;
+  const int T = (rpw + 15) / 16;
+  if (T == 1) return launch_ring_t<BF16, OUT_DT, 1>(x, M, nib, sc, out, N, K, rpw, s);
+  if (T == 2) return launch_ring_t<BF16, OUT_DT, 2>(x, M, nib, sc, out, N, K, rpw, s);
+  if (T == 3) return launch_ring_t<BF16, OUT_DT, 3>(x, M, nib, sc, out, N, K, rpw, s);
+  return launch_ring_t<BF16, OUT_DT, 4>(x, M, nib, sc, out, N, K, rpw, s);
+}
+
+static bool ring_fits(int M, int N, int K, const float* awq) {
+  return M <= kGemmSmallM && !awq && K % 128 == 0 && N <= 16384;
+}
+
 template <bool BF16, bool AWQ>
 static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
                                void* out, int out_dt, int N, int K, hipStream_t s) {
+  if (!AWQ && ring_fits(M, N, K, awq)) {
+    switch (out_dt) {
+      case NVE_DT_F16: return launch_ring_o<BF16, NVE_DT_F16>(x, M, nib, sc, out, N, K, s);
+      case NVE_DT_BF16: return launch_ring_o<BF16, NVE_DT_BF16>(x, M, nib, sc, out, N, K, s);
+      default: return launch_ring_o<BF16, NVE_DT_F32>(x, M, nib, sc, out, N, K, s);
+    }
+  }
   switch (out_dt) {
     case NVE_DT_F16: return launch_small_o<BF16, AWQ, NVE_DT_F16>(x, M, nib, sc, awq, out, N, K, s);
     case NVE_DT_BF16: return launch_small_o<BF16, AWQ, NVE_DT_BF16>(x, M, nib, sc, awq, out, N, K, s);
