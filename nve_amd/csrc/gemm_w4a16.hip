@@ -406,15 +406,15 @@ struct W16Ring {
   static constexpr int LOADS = 2 * T + EU;
 };
 
-template <bool BF16, int OUT_DT, int T, int EU>
-__global__ __launch_bounds__(1024) void gemm_w4a16_ring_kernel(const uint16_t* __restrict__ x,
+template <bool BF16, int OUT_DT, int T, int EU, int KS, int S>
+__global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t* __restrict__ x,
                                                                const uint8_t* __restrict__ nib,
                                                                const float* __restrict__ ws,
                                                                void* __restrict__ out, int M, int N, int K,
                                                                int rows_per_wg) {
-  constexpr int KS = 16;
+  static_assert(S >= 1 && S <= 2, "ring depth");
   using L = W16Ring<T, EU>;
-  constexpr int kRing = KS * L::SLOT;
+  constexpr int kRing = KS * S * L::SLOT;
   constexpr int kRed = KS * T * 16 * (4 * EU + 1) * 4;
   __shared__ __attribute__((aligned(16))) char smem[kRing > kRed ? kRing : kRed];
   const int lane = threadIdx.x & 63;
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(1024) void gemm_w4a16_ring_kernel(const uint16_t* _
   const int row0 = blockIdx.x * rows_per_wg;
   const int nb = K >> 5, nq = nb >> 2;
   const int nqw = (nq + KS - 1) / KS;
-  char* const ring = smem + wave * L::SLOT;
+  char* const ring = smem + wave * (S * L::SLOT);
 
   const uint8_t* wsrc[T];
   const float* ssrc[T];
@@ -448,15 +448,16 @@ __global__ __launch_bounds__(1024) void gemm_w4a16_ring_kernel(const uint16_t* _
   }
   auto issue = [&](int i) {
     const int q = min(wave + KS * i, nq - 1);
+    char* const sb = ring + (i % S) * L::SLOT;
 #pragma unroll
     for (int t = 0; t < T; ++t)
-      if (wok[t]) lds_dma16(wsrc[t] + 64 * q, ring + L::W + t * 1024);
+      if (wok[t]) lds_dma16(wsrc[t] + 64 * q, sb + L::W + t * 1024);
 #pragma unroll
     for (int t = 0; t < T; ++t)
-      if (wok[t]) lds_dma4(ssrc[t] + 4 * q, ring + L::SC + t * 256);
+      if (wok[t]) lds_dma4(ssrc[t] + 4 * q, sb + L::SC + t * 256);
 #pragma unroll
     for (int a = 0; a < EU; ++a)
-      if (aok[a]) lds_dma16(asrc[a] + 256 * q, ring + L::A + a * 1024);
+      if (aok[a]) lds_dma16(asrc[a] + 256 * q, sb + L::A + a * 1024);
   };
 
   // A row nl holds activation row am (rows >= M read row M - 1, never stored)
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(1024) void gemm_w4a16_ring_kernel(const uint16_t* _
 
   auto compute = [&](int i) {
     if (wave + KS * i >= nq) return;  // clamped duplicate quad (wave-uniform)
-    const uint32_t sb = lds_addr(ring);
+    const uint32_t sb = lds_addr(ring + (i % S) * L::SLOT);
     u32x2_t xl[4], xh[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -529,18 +530,26 @@ __global__ __launch_bounds__(1024) void gemm_w4a16_ring_kernel(const uint16_t* _
     }
   };
 
-  issue(0);
+  // S quads in flight: the transfers of quad i + S - 1 are issued before quad i is
+  // computed; every quad is the same LOADS transfers (clamped quads past the wave's
+  // share included), so the waits are exact.
+#pragma unroll
+  for (int k = 0; k < S; ++k)
+    if (k < nqw) issue(k);
   int i = 0;
-  for (; i + 1 < nqw; ++i) {
-    wait_vmcnt<0>();
+  for (; i + S < nqw; ++i) {
+    wait_vmcnt<(S - 1) * L::LOADS>();
     __builtin_amdgcn_sched_barrier(0);
     compute(i);
     __builtin_amdgcn_sched_barrier(0);
-    issue(i + 1);
+    issue(i + S);
   }
-  wait_vmcnt<0>();
-  __builtin_amdgcn_sched_barrier(0);
-  compute(i);
+  for (; i < nqw; ++i) {
+    if (i + 1 < nqw) wait_vmcnt<(S - 1) * L::LOADS>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i);
+  }
 
   __syncthreads();  // every wave is done with its slot: reuse the LDS for the reduction
   float(*s_red)[T * 16][4 * EU + 1] = (float(*)[T * 16][4 * EU + 1])smem;
@@ -670,9 +679,12 @@ template <bool BF16, int OUT_DT, int T>
 static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
                                 int rpw, hipStream_t s) {
   const dim3 grid((N + rpw - 1) / rpw);
+  // 16 waves, one quad in flight each (8B gate, fp16 x, M = 1 / 4 / 16: 12.1 / 11.9-12.1 /
+  // 12.5-12.8 us; 8 waves with two quads in flight 12.6 / 12.5-12.6 / 13.3-13.4, 8 waves
+  // with one 13.4-13.7 / 13.1 / 13.9-14.0)
 #define NVE_R16(EU) \
-  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, OUT_DT, T, EU>), grid, dim3(1024), 0, s, (const uint16_t*)x, \
-                     nib, sc, out, M, N, K, rpw)
+  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, OUT_DT, T, EU, 16, 1>), grid, dim3(1024), 0, s, \
+                     (const uint16_t*)x, nib, sc, out, M, N, K, rpw)
   if (M <= 4) NVE_R16(1);
   else if (M <= 8) NVE_R16(2);
   else NVE_R16(4);
