@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
   }
 }
 
-// ---- small M (M <= 16), K % 128 == 0, no AWQ: the LDS-ring form ----------------------
+// ---- small M (M <= 16), K % 128 == 0: the LDS-ring form ------------------------------
 // The weight-streaming kernel above with the W4A8 batched kernel's LDS ring
 // (gemv_w4a8_batched.hip) in place of its VGPR loads and ds_bpermute moves: every load
 // is a global -> LDS transfer into a per-wave slot holding one K quad --
@@ -400,20 +400,23 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
 // One quad in flight per wave, 16 waves; workgroups take ceil(N / 256) rows each (one
 // per CU), the last tile partly masked (masked lanes issue no transfers; lane 0 always
 // does, so every wave instruction counts once and the vmcnt waits are exact).
-template <int T, int EU>
+//   AW 512 B       (AWQ) the quad's 128 activation-scale factors, one transfer of 32 lanes
+template <int T, int EU, bool AWQ>
 struct W16Ring {
-  static constexpr int W = 0, SC = T * 1024, A = SC + T * 256, SLOT = A + EU * 1024;
-  static constexpr int LOADS = 2 * T + EU;
+  static constexpr int W = 0, SC = T * 1024, A = SC + T * 256, AW = A + EU * 1024;
+  static constexpr int SLOT = AW + (AWQ ? 512 : 0);
+  static constexpr int LOADS = 2 * T + EU + (AWQ ? 1 : 0);
 };
 
-template <bool BF16, int OUT_DT, int T, int EU, int KS, int S>
+template <bool BF16, bool AWQ, int OUT_DT, int T, int EU, int KS, int S>
 __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t* __restrict__ x,
                                                                const uint8_t* __restrict__ nib,
                                                                const float* __restrict__ ws,
+                                                               const float* __restrict__ awq,
                                                                void* __restrict__ out, int M, int N, int K,
                                                                int rows_per_wg) {
   static_assert(S >= 1 && S <= 2, "ring depth");
-  using L = W16Ring<T, EU>;
+  using L = W16Ring<T, EU, AWQ>;
   constexpr int kRing = KS * S * L::SLOT;
   constexpr int kRed = KS * T * 16 * (4 * EU + 1) * 4;
   __shared__ __attribute__((aligned(16))) char smem[kRing > kRed ? kRing : kRed];
@@ -458,6 +461,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
 #pragma unroll
     for (int a = 0; a < EU; ++a)
       if (aok[a]) lds_dma16(asrc[a] + 256 * q, sb + L::A + a * 1024);
+    if (AWQ && lane < 32) lds_dma16(awq + 128 * q + 4 * lane, sb + L::AW);
   };
 
   // A row nl holds activation row am (rows >= M read row M - 1, never stored)
@@ -492,7 +496,23 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
       wr[t] = ds_read128(sb + L::W + t * 1024 + rd_w);
       sr[t] = ds_read128(sb + L::SC + t * 256 + nl * 16);
     }
+    // awq at the lane's k-runs of each block
+    u32x4_t al[AWQ ? 4 : 1], ah[AWQ ? 4 : 1];
+    if constexpr (AWQ) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        al[j] = ds_read128(sb + L::AW + 4 * (32 * j + 4 * g));
+        ah[j] = ds_read128(sb + L::AW + 4 * (32 * j + 16 + 4 * g));
+      }
+    }
     lgkm_wait();
+    if constexpr (AWQ) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tie(al[j]);
+        tie(ah[j]);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       tie(xl[j]);
@@ -522,6 +542,15 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
         for (int e = 0; e < 4; ++e) {
           v[e] = fmaf((float)((lo >> (8 * e)) & 0xffu), s, s8);
           v[4 + e] = fmaf((float)((hi >> (8 * e)) & 0xffu), s, s8);
+        }
+        if constexpr (AWQ) {
+          const uint32_t l4[4] = {al[j].x, al[j].y, al[j].z, al[j].w};
+          const uint32_t h4[4] = {ah[j].x, ah[j].y, ah[j].z, ah[j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] *= __uint_as_float(l4[e]);
+            v[4 + e] *= __uint_as_float(h4[e]);
+          }
         }
         const uint4 b = make_uint4(cvt_pk<BF16>(v[0], v[1]), cvt_pk<BF16>(v[2], v[3]), cvt_pk<BF16>(v[4], v[5]),
                                    cvt_pk<BF16>(v[6], v[7]));
@@ -673,18 +702,18 @@ static hipError_t launch_small_o(const void* x, int M, const uint8_t* nib, const
   return hipGetLastError();
 }
 
-// M <= 16 without AWQ, K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
+// M <= 16, K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
 // rows per workgroup (16 below 4096 rows), one activation transfer per 4 rows of M.
-template <bool BF16, int OUT_DT, int T>
-static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
-                                int rpw, hipStream_t s) {
+template <bool BF16, bool AWQ, int OUT_DT, int T>
+static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq, void* out,
+                                int N, int K, int rpw, hipStream_t s) {
   const dim3 grid((N + rpw - 1) / rpw);
   // 16 waves, one quad in flight each (8B gate, fp16 x, M = 1 / 4 / 16: 12.1 / 11.9-12.1 /
   // 12.5-12.8 us; 8 waves with two quads in flight 12.6 / 12.5-12.6 / 13.3-13.4, 8 waves
   // with one 13.4-13.7 / 13.1 / 13.9-14.0)
 #define NVE_R16(EU) \
-  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, OUT_DT, T, EU, 16, 1>), grid, dim3(1024), 0, s, \
-                     (const uint16_t*)x, nib, sc, out, M, N, K, rpw)
+  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, AWQ, OUT_DT, T, EU, 16, 1>), grid, dim3(1024), 0, s, \
+                     (const uint16_t*)x, nib, sc, awq, out, M, N, K, rpw)
   if (M <= 4) NVE_R16(1);
   else if (M <= 8) NVE_R16(2);
   else NVE_R16(4);
@@ -692,29 +721,27 @@ static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const 
   return hipGetLastError();
 }
 
-template <bool BF16, int OUT_DT>
-static hipError_t launch_ring_o(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
-                                hipStream_t s) {
+template <bool BF16, bool AWQ, int OUT_DT>
+static hipError_t launch_ring_o(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq, void* out,
+                                int N, int K, hipStream_t s) {
   const int rpw = N <= 4096 ? 16 : (N + 255) / 256;
   const int T = (rpw + 15) / 16;
-  if (T == 1) return launch_ring_t<BF16, OUT_DT, 1>(x, M, nib, sc, out, N, K, rpw, s);
-  if (T == 2) return launch_ring_t<BF16, OUT_DT, 2>(x, M, nib, sc, out, N, K, rpw, s);
-  if (T == 3) return launch_ring_t<BF16, OUT_DT, 3>(x, M, nib, sc, out, N, K, rpw, s);
-  return launch_ring_t<BF16, OUT_DT, 4>(x, M, nib, sc, out, N, K, rpw, s);
+  if (T == 1) return launch_ring_t<BF16, AWQ, OUT_DT, 1>(x, M, nib, sc, awq, out, N, K, rpw, s);
+  if (T == 2) return launch_ring_t<BF16, AWQ, OUT_DT, 2>(x, M, nib, sc, awq, out, N, K, rpw, s);
+  if (T == 3) return launch_ring_t<BF16, AWQ, OUT_DT, 3>(x, M, nib, sc, awq, out, N, K, rpw, s);
+  return launch_ring_t<BF16, AWQ, OUT_DT, 4>(x, M, nib, sc, awq, out, N, K, rpw, s);
 }
 
-static bool ring_fits(int M, int N, int K, const float* awq) {
-  return M <= kGemmSmallM && !awq && K % 128 == 0 && N <= 16384;
-}
+static bool ring_fits(int M, int N, int K) { return M <= kGemmSmallM && K % 128 == 0 && N <= 16384; }
 
 template <bool BF16, bool AWQ>
 static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
                                void* out, int out_dt, int N, int K, hipStream_t s) {
-  if (!AWQ && ring_fits(M, N, K, awq)) {
+  if (ring_fits(M, N, K)) {
     switch (out_dt) {
-      case NVE_DT_F16: return launch_ring_o<BF16, NVE_DT_F16>(x, M, nib, sc, out, N, K, s);
-      case NVE_DT_BF16: return launch_ring_o<BF16, NVE_DT_BF16>(x, M, nib, sc, out, N, K, s);
-      default: return launch_ring_o<BF16, NVE_DT_F32>(x, M, nib, sc, out, N, K, s);
+      case NVE_DT_F16: return launch_ring_o<BF16, AWQ, NVE_DT_F16>(x, M, nib, sc, awq, out, N, K, s);
+      case NVE_DT_BF16: return launch_ring_o<BF16, AWQ, NVE_DT_BF16>(x, M, nib, sc, awq, out, N, K, s);
+      default: return launch_ring_o<BF16, AWQ, NVE_DT_F32>(x, M, nib, sc, awq, out, N, K, s);
     }
   }
   switch (out_dt) {

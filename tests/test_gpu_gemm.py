@@ -90,7 +90,7 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
     """M <= 16 runs a weight-streaming kernel: 16 rows of the identity at a time
     (X = I[k0 : k0 + 16]) read back 16 columns of the weight matrix as the kernel
     rounded it, which must equal the reference dequant bit for bit.  K = 448 leaves a
-    partial last quad of blocks (the register kernel); K = 512 without AWQ runs the
+    partial last quad of blocks (the register kernel); K = 512 and 256 run the
     LDS-ring kernel (16-row workgroups at 70 rows, 17-row workgroups at 4100: a partly
     masked second tile)."""
     torch = torch_dev
