@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
   }
 }
 
-// ---- small M (M <= 16), K % 128 == 0: the LDS-ring form ------------------------------
+// ---- small M (M <= 32), K % 128 == 0: the LDS-ring form ------------------------------
 // The weight-streaming kernel above with the W4A8 batched kernel's LDS ring
 // (gemv_w4a8_batched.hip) in place of its VGPR loads and ds_bpermute moves: every load
 // is a global -> LDS transfer into a per-wave slot holding one K quad --
@@ -417,6 +417,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
                                                                int rows_per_wg) {
   static_assert(S >= 1 && S <= 2, "ring depth");
   using L = W16Ring<T, EU, AWQ>;
+  // EU activation transfers of 4 rows: up to 16 rows form one A operand group, 32 rows
+  // (EU = 8) two groups that share every dequantized weight fragment
+  constexpr int MG = EU > 4 ? 2 : 1, EG = EU > 4 ? 4 : EU;
   constexpr int kRing = KS * S * L::SLOT;
   constexpr int kRed = KS * T * 16 * (4 * EU + 1) * 4;
   __shared__ __attribute__((aligned(16))) char smem[kRing > kRed ? kRing : kRed];
@@ -464,32 +467,38 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
     if (AWQ && lane < 32) lds_dma16(awq + 128 * q + 4 * lane, sb + L::AW);
   };
 
-  // A row nl holds activation row am (rows >= M read row M - 1, never stored)
+  // A row nl of group G holds activation row 16 G + am (rows >= M read row M - 1,
+  // never stored)
   const int am = 4 * (nl & 3) + (nl >> 2);
-  const int ar = min(am, M - 1);
   const uint32_t rd_w = 16 * (4 * nl + ((g + (nl >> 1)) & 3));
-  uint32_t rd_lo[4], rd_hi[4];
-  {
+  uint32_t rd_lo[MG][4], rd_hi[MG][4];
+#pragma unroll
+  for (int G = 0; G < MG; ++G) {
+    const int ar = min(16 * G + am, M - 1);
     const uint32_t rb = L::A + (ar >> 2) * 1024 + (ar & 3) * 256 + 8 * (g & 1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      rd_lo[j] = rb + 16 * ((4 * j + (g >> 1)) ^ (ar & 15));
-      rd_hi[j] = rb + 16 * ((4 * j + 2 + (g >> 1)) ^ (ar & 15));
+      rd_lo[G][j] = rb + 16 * ((4 * j + (g >> 1)) ^ (ar & 15));
+      rd_hi[G][j] = rb + 16 * ((4 * j + 2 + (g >> 1)) ^ (ar & 15));
     }
   }
-  f4_t acc[T];
+  f4_t acc[T][MG];
 #pragma unroll
-  for (int t = 0; t < T; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int G = 0; G < MG; ++G) acc[t][G] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](int i) {
     if (wave + KS * i >= nq) return;  // clamped duplicate quad (wave-uniform)
     const uint32_t sb = lds_addr(ring + (i % S) * L::SLOT);
-    u32x2_t xl[4], xh[4];
+    u32x2_t xl[MG][4], xh[MG][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      xl[j] = ds_read64(sb + rd_lo[j]);
-      xh[j] = ds_read64(sb + rd_hi[j]);
-    }
+    for (int G = 0; G < MG; ++G)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xl[G][j] = ds_read64(sb + rd_lo[G][j]);
+        xh[G][j] = ds_read64(sb + rd_hi[G][j]);
+      }
     u32x4_t wr[T], sr[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -514,18 +523,22 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      tie(xl[j]);
-      tie(xh[j]);
-    }
+    for (int G = 0; G < MG; ++G)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tie(xl[G][j]);
+        tie(xh[G][j]);
+      }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       tie(wr[t]);
       tie(sr[t]);
     }
-    uint4 a[4];
+    uint4 a[MG][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a[j] = make_uint4(xl[j].x, xl[j].y, xh[j].x, xh[j].y);
+    for (int G = 0; G < MG; ++G)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[G][j] = make_uint4(xl[G][j].x, xl[G][j].y, xh[G][j].x, xh[G][j].y);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       uint32_t c0 = wr[t].x, c1 = wr[t].y, c2 = wr[t].z, c3 = wr[t].w;
@@ -554,7 +567,8 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
         }
         const uint4 b = make_uint4(cvt_pk<BF16>(v[0], v[1]), cvt_pk<BF16>(v[2], v[3]), cvt_pk<BF16>(v[4], v[5]),
                                    cvt_pk<BF16>(v[6], v[7]));
-        acc[t] = mfma16<BF16>(a[j], b, acc[t]);
+#pragma unroll
+        for (int G = 0; G < MG; ++G) acc[t][G] = mfma16<BF16>(a[G][j], b, acc[t][G]);
       }
     }
   };
@@ -582,11 +596,14 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
 
   __syncthreads();  // every wave is done with its slot: reuse the LDS for the reduction
   float(*s_red)[T * 16][4 * EU + 1] = (float(*)[T * 16][4 * EU + 1])smem;
-  // D layout: lane (n, g) holds rows i = 4g + e (activation row 4e + g) of column n
+  // D layout: lane (n, g) of group G holds rows i = 4g + e (activation row
+  // 16 G + 4e + g) of column n
 #pragma unroll
   for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int e = 0; e < EU; ++e) s_red[wave][16 * t + nl][4 * e + g] = acc[t][e];
+    for (int G = 0; G < MG; ++G)
+#pragma unroll
+      for (int e = 0; e < EG; ++e) s_red[wave][16 * t + nl][16 * G + 4 * e + g] = acc[t][G][e];
   __syncthreads();
   const int rows = min(rows_per_wg, N - row0);
   for (int xi = threadIdx.x; xi < T * 16 * 4 * EU; xi += 64 * KS) {
@@ -702,7 +719,7 @@ static hipError_t launch_small_o(const void* x, int M, const uint8_t* nib, const
   return hipGetLastError();
 }
 
-// M <= 16, K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
+// M <= 32, K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
 // rows per workgroup (16 below 4096 rows), one activation transfer per 4 rows of M.
 template <bool BF16, bool AWQ, int OUT_DT, int T>
 static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq, void* out,
@@ -711,12 +728,15 @@ static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const 
   // 16 waves, one quad in flight each (8B gate, fp16 x, M = 1 / 4 / 16: 12.1 / 11.9-12.1 /
   // 12.5-12.8 us; 8 waves with two quads in flight 12.6 / 12.5-12.6 / 13.3-13.4, 8 waves
   // with one 13.4-13.7 / 13.1 / 13.9-14.0)
-#define NVE_R16(EU) \
-  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, AWQ, OUT_DT, T, EU, 16, 1>), grid, dim3(1024), 0, s, \
+  // M = 17-32: two 16-row operand groups per dequantized weight fragment; their 8 KiB of
+  // activation rows per slot leave LDS for 8 waves
+#define NVE_R16(EU, KS) \
+  hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, AWQ, OUT_DT, T, EU, KS, 1>), grid, dim3(64 * KS), 0, s, \
                      (const uint16_t*)x, nib, sc, awq, out, M, N, K, rpw)
-  if (M <= 4) NVE_R16(1);
-  else if (M <= 8) NVE_R16(2);
-  else NVE_R16(4);
+  if (M <= 4) NVE_R16(1, 16);
+  else if (M <= 8) NVE_R16(2, 16);
+  else if (M <= 16) NVE_R16(4, 16);
+  else NVE_R16(8, 8);
 #undef NVE_R16
   return hipGetLastError();
 }
@@ -732,7 +752,8 @@ static hipError_t launch_ring_o(const void* x, int M, const uint8_t* nib, const 
   return launch_ring_t<BF16, AWQ, OUT_DT, 4>(x, M, nib, sc, awq, out, N, K, rpw, s);
 }
 
-static bool ring_fits(int M, int N, int K) { return M <= kGemmSmallM && K % 128 == 0 && N <= 16384; }
+constexpr int kGemmRingM = 32;
+static bool ring_fits(int M, int N, int K) { return M <= kGemmRingM && K % 128 == 0 && N <= 16384; }
 
 template <bool BF16, bool AWQ>
 static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
@@ -755,7 +776,7 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
-  if (M <= kGemmSmallM) {
+  if (M <= kGemmSmallM || ring_fits(M, N, K)) {
     if (awq) return bf ? launch_small<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, s)
                        : launch_small<false, true>(x, M, nib, sc, awq, out, out_dt, N, K, s);
     return bf ? launch_small<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, s)

@@ -42,6 +42,7 @@ def _round(a, dt):
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (2, 1000, 4096), (16, 200, 192), (16, 8200, 1024),
                                    (1, 4097, 256), (4, 14336, 4096), (9, 4096, 14336), (16, 16384, 512),
+                                   (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256),
                                    (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
@@ -85,16 +86,16 @@ def test_gemm_w4a16_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_
 
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
-@pytest.mark.parametrize("n,k", [(70, 448), (70, 512), (4100, 256)])
-def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_awq, n, k):
-    """M <= 16 runs a weight-streaming kernel: 16 rows of the identity at a time
-    (X = I[k0 : k0 + 16]) read back 16 columns of the weight matrix as the kernel
+@pytest.mark.parametrize("n,k,mb", [(70, 448, 16), (70, 512, 16), (4100, 256, 16), (70, 512, 32), (4100, 256, 24)])
+def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_awq, n, k, mb):
+    """M <= 32 runs a weight-streaming kernel: mb rows of the identity at a time
+    (X = I[k0 : k0 + mb]) read back mb columns of the weight matrix as the kernel
     rounded it, which must equal the reference dequant bit for bit.  K = 448 leaves a
-    partial last quad of blocks (the register kernel); K = 512 and 256 run the
+    partial last quad of blocks (the register kernel, M <= 16); K = 512 and 256 run the
     LDS-ring kernel (16-row workgroups at 70 rows, 17-row workgroups at 4100: a partly
-    masked second tile)."""
+    masked second tile; mb = 24 / 32: two operand groups of activation rows)."""
     torch = torch_dev
-    print(f"identity n={n} k={k} x={xdt} awq={with_awq}", flush=True)
+    print(f"identity n={n} k={k} mb={mb} x={xdt} awq={with_awq}", flush=True)
     data = orc.q4_from_f32(weights(n, k, seed=41, std=0.3))
     nib, sc = orc.extract_for_gpu(data, n, k)
     awq = np.random.default_rng(42).uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
@@ -104,9 +105,9 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
     tn, ts = torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda()
     ta = None if awq is None else torch.from_numpy(awq).cuda()
     got = np.zeros((k, n), np.float32)
-    for k0 in range(0, k, 16):
-        y = hk.gemm_w4a16(eye[k0:k0 + 16].contiguous(), tn, ts, n, k, ta, out_dtype=torch.float32)
-        got[k0:k0 + 16] = y.cpu().numpy()
+    for k0 in range(0, k, mb):
+        y = hk.gemm_w4a16(eye[k0:k0 + mb].contiguous(), tn, ts, n, k, ta, out_dtype=torch.float32)
+        got[k0:k0 + mb] = y.cpu().numpy()
     torch.cuda.synchronize()
     assert np.array_equal(got.T.view(np.uint32), wref.view(np.uint32))
 
