@@ -42,7 +42,8 @@ def _round(a, dt):
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (2, 1000, 4096), (16, 200, 192), (16, 8200, 1024),
                                    (1, 4097, 256), (4, 14336, 4096), (9, 4096, 14336), (16, 16384, 512),
-                                   (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256),
+                                   (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256), (48, 14336, 4096),
+                                   (100, 2000, 1024),
                                    (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
@@ -86,7 +87,7 @@ def test_gemm_w4a16_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_
 
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
-@pytest.mark.parametrize("n,k,mb", [(70, 448, 16), (70, 512, 16), (4100, 256, 16), (70, 512, 32), (4100, 256, 24)])
+@pytest.mark.parametrize("n,k,mb", [(70, 448, 16), (70, 512, 16), (4100, 256, 16), (70, 512, 32), (4100, 256, 24), (70, 512, 48)])
 def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_awq, n, k, mb):
     """M <= 32 runs a weight-streaming kernel: mb rows of the identity at a time
     (X = I[k0 : k0 + mb]) read back mb columns of the weight matrix as the kernel
@@ -215,7 +216,7 @@ def test_gemm_w4a16_ws_graph_capture(orc, torch_dev, hk):
                 assert torch.equal(out, eager_fused)
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 512, 4096), (40, 1000, 2048), (200, 256, 8192)])
+@pytest.mark.parametrize("m,n,k", [(64, 512, 4160), (40, 1000, 2112), (200, 256, 8192)])
 def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
     """With a workspace, a K-split fp32 product stores its partials there and adds them
     in a fixed order: every call -- eager or replayed from a HIP graph -- gives the same
