@@ -625,7 +625,9 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
                             "frac_mfma_peak": round(fl / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
                             "dequant_plus_blas_us": round(us_ref, 1),
                             "library_us": round(us_lib, 1),
-                            "library_path": "dequant + hipBLASLt" if wsb else "fused"})
+                            # the library's rule (gemm_blas.hip): dequant + hipBLASLt from M = 512
+                            # with a workspace; below it the workspace holds K-split partials
+                            "library_path": "dequant + hipBLASLt" if m >= 512 and wsb else "fused"})
         log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us, "
             f"nve_hip_gemm_w4a16_ws {us_lib:.1f} us")
         del x, wf, ws
