@@ -392,15 +392,16 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
 //   A  EU x 1 KiB  activation rows 4a..4a+3 of the quad, 256 B each (4 blocks of 32
 //                  fp16 / bf16), the 16-byte pieces of row r stored at piece ^ (r & 15)
 //                  so that the 16 rows' reads of one k-set fall on different banks
+//   AW 512 B       (AWQ) the quad's 128 activation-scale factors, one transfer of 32 lanes
 // -- and the operand lanes read the slot: the weight piece (ds_read_b128 and the 4x4
 // permlane transpose: nibble dword g of the 4 blocks), the row's scales, and per block
 // the two 8-byte k-runs {4g..4g+3} and {16+4g..16+4g+3} of the activation row.  The
 // nibbles are extracted low / high per byte, which yields that same k order, so the B
 // operand (the reference dequant f16/bf16(fma(n, s, -8 s)), as above) needs no permute.
-// One quad in flight per wave, 16 waves; workgroups take ceil(N / 256) rows each (one
-// per CU), the last tile partly masked (masked lanes issue no transfers; lane 0 always
-// does, so every wave instruction counts once and the vmcnt waits are exact).
-//   AW 512 B       (AWQ) the quad's 128 activation-scale factors, one transfer of 32 lanes
+// KS waves with S quads in flight each (the launcher: 16 waves, one quad; 8 waves where
+// 32 activation rows form two operand groups); workgroups take ceil(N / 256) rows each
+// (one per CU), the last tile partly masked (masked lanes issue no transfers; lane 0
+// always does, so every wave instruction counts once and the vmcnt waits are exact).
 template <int T, int EU, bool AWQ>
 struct W16Ring {
   static constexpr int W = 0, SC = T * 1024, A = SC + T * 256, AW = A + EU * 1024;
