@@ -757,6 +757,8 @@ def main():
     ap.add_argument("--suite-probe", action="store_true",
                     help="only the per-shape 8B table and the batched sweep, for rocprofv3 --kernel-trace "
                          "per-shape kernel durations (no bench line)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the W4A16 prefill GEMM rows (for profiling; no bench line)")
     ap.add_argument("--decode-traffic-probe", action="store_true",
                     help="6 eager (not graph-replayed) 3B decode steps for rocprofv3 --pmc (no bench line)")
     args = ap.parse_args()
@@ -784,6 +786,9 @@ def main():
         return
     if args.suite_probe:
         suite_probe(torch, L, hk)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill_w4a16_gemm": prefill_gemm(torch, hk)}))
         return
     if args.decode_only:
         print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True,
