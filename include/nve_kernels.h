@@ -227,7 +227,7 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * then a dense GEMM) in one kernel: each weight is rounded exactly as the dequant
  * rounds it (to x's dtype: F16 as the reference, or BF16) and the products accumulate
  * in fp32 on MFMA (M <= 128: weight-streaming kernels, where K % 128 == 0 and N <= 16384 an
- * LDS ring in launches of up to 32 rows, else M <= 16 only; larger M: LDS-tiled).  x [M, K]
+ * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; larger M: LDS-tiled).  x [M, K]
  * row-major F16/BF16 (16-byte aligned); awq [K] or NULL; out [M, N] row-major F16,
  * BF16 or F32.  K % 64 == 0.  With F32 output and a tile grid too small to fill the
  * GPU, K is split over workgroups whose fp32 partials are added atomically: the last

@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_small_kernel(const uint16_
   }
 }
 
-// ---- small M (M <= 32), K % 128 == 0: the LDS-ring form ------------------------------
+// ---- small M (M <= 64), K % 128 == 0: the LDS-ring form ------------------------------
 // The weight-streaming kernel above with the W4A8 batched kernel's LDS ring
 // (gemv_w4a8_batched.hip) in place of its VGPR loads and ds_bpermute moves: every load
 // is a global -> LDS transfer into a per-wave slot holding one K quad --
@@ -418,9 +418,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_w4a16_ring_kernel(const uint16_t
                                                                int rows_per_wg) {
   static_assert(S >= 1 && S <= 2, "ring depth");
   using L = W16Ring<T, EU, AWQ>;
-  // EU activation transfers of 4 rows: up to 16 rows form one A operand group, 32 rows
-  // (EU = 8) two groups that share every dequantized weight fragment
-  constexpr int MG = EU > 4 ? 2 : 1, EG = EU > 4 ? 4 : EU;
+  // EU activation transfers of 4 rows: up to 16 rows form one A operand group, 32 / 64
+  // rows (EU = 8 / 16) two / four groups that share every dequantized weight fragment
+  constexpr int MG = EU > 4 ? EU / 4 : 1, EG = EU > 4 ? 4 : EU;
   constexpr int kRing = KS * S * L::SLOT;
   constexpr int kRed = KS * T * 16 * (4 * EU + 1) * 4;
   __shared__ __attribute__((aligned(16))) char smem[kRing > kRed ? kRing : kRed];
@@ -720,7 +720,7 @@ static hipError_t launch_small_o(const void* x, int M, const uint8_t* nib, const
   return hipGetLastError();
 }
 
-// M <= 32, K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
+// M <= 64 (32 with AWQ), K % 128 == 0, N <= 16384: the LDS-ring kernel, ceil(N / 256)
 // rows per workgroup (16 below 4096 rows), one activation transfer per 4 rows of M.
 template <bool BF16, bool AWQ, int OUT_DT, int T>
 static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq, void* out,
@@ -729,15 +729,17 @@ static hipError_t launch_ring_t(const void* x, int M, const uint8_t* nib, const 
   // 16 waves, one quad in flight each (8B gate, fp16 x, M = 1 / 4 / 16: 12.1 / 11.9-12.1 /
   // 12.5-12.8 us; 8 waves with two quads in flight 12.6 / 12.5-12.6 / 13.3-13.4, 8 waves
   // with one 13.4-13.7 / 13.1 / 13.9-14.0)
-  // M = 17-32: two 16-row operand groups per dequantized weight fragment; their 8 KiB of
-  // activation rows per slot leave LDS for 8 waves
+  // M = 17-32 / 33-64: two / four 16-row operand groups per dequantized weight fragment;
+  // their 8 / 16 KiB of activation rows per slot leave LDS for 8 / 6 waves (four groups
+  // without AWQ only: with it the kernel needs more than 256 VGPRs)
 #define NVE_R16(EU, KS) \
   hipLaunchKernelGGL((nve::gemm_w4a16_ring_kernel<BF16, AWQ, OUT_DT, T, EU, KS, 1>), grid, dim3(64 * KS), 0, s, \
                      (const uint16_t*)x, nib, sc, awq, out, M, N, K, rpw)
   if (M <= 4) NVE_R16(1, 16);
   else if (M <= 8) NVE_R16(2, 16);
   else if (M <= 16) NVE_R16(4, 16);
-  else NVE_R16(8, 8);
+  else if (AWQ || M <= 32) NVE_R16(8, 8);
+  else if constexpr (!AWQ) NVE_R16(16, 6);
 #undef NVE_R16
   return hipGetLastError();
 }
@@ -753,13 +755,18 @@ static hipError_t launch_ring_o(const void* x, int M, const uint8_t* nib, const 
   return launch_ring_t<BF16, AWQ, OUT_DT, 4>(x, M, nib, sc, awq, out, N, K, rpw, s);
 }
 
-constexpr int kGemmRingM = 32;
-static bool ring_fits(int M, int N, int K) { return M <= kGemmRingM && K % 128 == 0 && N <= 16384; }
+// rows one ring launch takes (without / with AWQ) and the M up to which launches of that
+// many rows beat the tiled kernel
+static int ring_rows(bool awq) { return awq ? 32 : 64; }
+constexpr int kGemmRingChunkedM = 128;
+static bool ring_fits(int M, int N, int K, bool awq) {
+  return M <= ring_rows(awq) && K % 128 == 0 && N <= 16384;
+}
 
 template <bool BF16, bool AWQ>
 static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
                                void* out, int out_dt, int N, int K, hipStream_t s) {
-  if (ring_fits(M, N, K)) {
+  if (ring_fits(M, N, K, AWQ)) {
     switch (out_dt) {
       case NVE_DT_F16: return launch_ring_o<BF16, AWQ, NVE_DT_F16>(x, M, nib, sc, awq, out, N, K, s);
       case NVE_DT_BF16: return launch_ring_o<BF16, AWQ, NVE_DT_BF16>(x, M, nib, sc, awq, out, N, K, s);
@@ -777,13 +784,15 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
-  // M = 33-128 where the ring fits: ring launches of up to 32 activation rows each (8B
-  // gate: 27 us at M = 48 and about 58 us at 128, against 45 / 71 us for the tiled
-  // kernel); a row's result does not depend on the rows launched with it
-  if (M > kGemmRingM && M <= 4 * kGemmRingM && ring_fits(kGemmRingM, N, K)) {
+  // up to M = 128 where the ring fits: ring launches of up to 64 (AWQ: 32) activation
+  // rows each (8B gate, 32-row launches: 27 us at M = 48 and about 58 us at 128, against
+  // 45 / 71 us for the tiled kernel); a row's result does not depend on the rows
+  // launched with it
+  const int rr = ring_rows(awq != nullptr);
+  if (M > rr && M <= kGemmRingChunkedM && ring_fits(rr, N, K, awq != nullptr)) {
     const size_t osz = out_dt == NVE_DT_F32 ? 4 : 2;
-    for (int m0 = 0; m0 < M; m0 += kGemmRingM) {
-      const int mc = M - m0 < kGemmRingM ? M - m0 : kGemmRingM;
+    for (int m0 = 0; m0 < M; m0 += rr) {
+      const int mc = M - m0 < rr ? M - m0 : rr;
       const void* xc = (const char*)x + (size_t)m0 * K * 2;
       void* oc = (char*)out + (size_t)m0 * N * osz;
       hipError_t e;
@@ -795,7 +804,7 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
     }
     return hipSuccess;
   }
-  if (M <= kGemmSmallM || ring_fits(M, N, K)) {
+  if (M <= kGemmSmallM || ring_fits(M, N, K, awq != nullptr)) {
     if (awq) return bf ? launch_small<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, s)
                        : launch_small<false, true>(x, M, nib, sc, awq, out, out_dt, N, K, s);
     return bf ? launch_small<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, s)

@@ -43,7 +43,7 @@ def _round(a, dt):
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (2, 1000, 4096), (16, 200, 192), (16, 8200, 1024),
                                    (1, 4097, 256), (4, 14336, 4096), (9, 4096, 14336), (16, 16384, 512),
                                    (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256), (48, 14336, 4096),
-                                   (100, 2000, 1024), (48, 16400, 512), (33, 200, 4160),
+                                   (100, 2000, 1024), (48, 16400, 512), (33, 200, 4160), (64, 14336, 4096), (60, 300, 512),
                                    (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
@@ -87,14 +87,15 @@ def test_gemm_w4a16_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_
 
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
-@pytest.mark.parametrize("n,k,mb", [(70, 448, 16), (70, 512, 16), (4100, 256, 16), (70, 512, 32), (4100, 256, 24), (70, 512, 48)])
+@pytest.mark.parametrize("n,k,mb", [(70, 448, 16), (70, 512, 16), (4100, 256, 16), (70, 512, 32), (4100, 256, 24), (70, 512, 48), (70, 512, 64)])
 def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xdt, with_awq, n, k, mb):
     """M <= 32 runs a weight-streaming kernel: mb rows of the identity at a time
     (X = I[k0 : k0 + mb]) read back mb columns of the weight matrix as the kernel
     rounded it, which must equal the reference dequant bit for bit.  K = 448 leaves a
     partial last quad of blocks (the register kernel, M <= 16); K = 512 and 256 run the
     LDS-ring kernel (16-row workgroups at 70 rows, 17-row workgroups at 4100: a partly
-    masked second tile; mb = 24 / 32: two operand groups of activation rows)."""
+    masked second tile; mb = 24 / 32: two operand groups of activation rows; mb = 64: four,
+    or two launches of 32 rows with AWQ)."""
     torch = torch_dev
     print(f"identity n={n} k={k} mb={mb} x={xdt} awq={with_awq}", flush=True)
     data = orc.q4_from_f32(weights(n, k, seed=41, std=0.3))
