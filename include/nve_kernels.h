@@ -226,7 +226,7 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * GpuWeight::matmul_x for seq > 1, src/gpu_layer.rs:219-237: nve_dequant_w4a16 to fp16
  * then a dense GEMM) in one kernel: each weight is rounded exactly as the dequant
  * rounds it (to x's dtype: F16 as the reference, or BF16) and the products accumulate
- * in fp32 on MFMA (M <= 128: weight-streaming kernels, where K % 128 == 0 and N <= 16384 an
+ * in fp32 on MFMA (M <= 320: weight-streaming kernels, where K % 128 == 0 and N <= 16384 an
  * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; larger M: LDS-tiled).  x [M, K]
  * row-major F16/BF16 (16-byte aligned); awq [K] or NULL; out [M, N] row-major F16,
  * BF16 or F32.  K % 64 == 0.  With F32 output and a tile grid too small to fill the

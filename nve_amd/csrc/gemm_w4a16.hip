@@ -758,7 +758,10 @@ static hipError_t launch_ring_o(const void* x, int M, const uint8_t* nib, const 
 // rows one ring launch takes (without / with AWQ) and the M up to which launches of that
 // many rows beat the tiled kernel
 static int ring_rows(bool awq) { return awq ? 32 : 64; }
-constexpr int kGemmRingChunkedM = 128;
+// 8B gate, 64-row launches: 62.5 / 83.0 / 103.7 / 124.5 us at M = 192 / 256 / 320 / 384
+// against 76.7 / 88.1 / 109.8 / 116.4 for the tiled kernel; 32-row launches (AWQ) stop
+// winning above 128 rows
+static int ring_chunked_max(bool awq) { return awq ? 128 : 320; }
 static bool ring_fits(int M, int N, int K, bool awq) {
   return M <= ring_rows(awq) && K % 128 == 0 && N <= 16384;
 }
@@ -784,12 +787,12 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
-  // up to M = 128 where the ring fits: ring launches of up to 64 (AWQ: 32) activation
-  // rows each (8B gate, 32-row launches: 27 us at M = 48 and about 58 us at 128, against
+  // up to M = 320 (AWQ: 128) where the ring fits: ring launches of up to 64 (AWQ: 32)
+  // activation rows each (8B gate, 32-row launches: 27 us at M = 48 and about 58 us at 128, against
   // 45 / 71 us for the tiled kernel); a row's result does not depend on the rows
   // launched with it
   const int rr = ring_rows(awq != nullptr);
-  if (M > rr && M <= kGemmRingChunkedM && ring_fits(rr, N, K, awq != nullptr)) {
+  if (M > rr && M <= ring_chunked_max(awq != nullptr) && ring_fits(rr, N, K, awq != nullptr)) {
     const size_t osz = out_dt == NVE_DT_F32 ? 4 : 2;
     for (int m0 = 0; m0 < M; m0 += rr) {
       const int mc = M - m0 < rr ? M - m0 : rr;

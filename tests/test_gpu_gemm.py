@@ -43,7 +43,7 @@ def _round(a, dt):
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 300, 4096), (2, 1000, 4096), (16, 200, 192), (16, 8200, 1024),
                                    (1, 4097, 256), (4, 14336, 4096), (9, 4096, 14336), (16, 16384, 512),
                                    (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256), (48, 14336, 4096),
-                                   (100, 2000, 1024), (48, 16400, 512), (33, 200, 4160), (64, 14336, 4096), (60, 300, 512),
+                                   (100, 2000, 1024), (48, 16400, 512), (33, 200, 4160), (64, 14336, 4096), (60, 300, 512), (320, 1000, 1024), (129, 700, 512),
                                    (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
