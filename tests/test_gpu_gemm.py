@@ -251,3 +251,31 @@ def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
     wref = _round(orc.q4_to_f32(data, n, k, None), "f16").astype(np.float64)
     ref = xh.astype(np.float64) @ wref.T
     assert rel_err_floor(a.cpu().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("m", [8, 48, 200])
+def test_gemm_w4a16_ring_graph_replay_matches_eager(orc, torch_dev, hk, m):
+    """The LDS-ring prefill path (one launch at M = 8 and 48, four 64-row launches at
+    M = 200) captured in a HIP graph: every replay, with eager work and
+    synchronisations between the replays, equals the eager call bit for bit."""
+    torch = torch_dev
+    n, k = 700, 1024
+    print(f"ring graph m={m}", flush=True)
+    data = orc.q4_from_f32(weights(n, k, seed=m, std=0.05))
+    nib_h, sc_h = orc.extract_for_gpu(data, n, k)
+    nib, sc = torch.from_numpy(nib_h).cuda(), torch.from_numpy(sc_h).cuda()
+    x = torch.from_numpy(np.random.default_rng(m).standard_normal((m, k)).astype(np.float16)).cuda()
+    eager = hk.gemm_w4a16(x, nib, sc, n, k, None, out_dtype=torch.float32)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out.copy_(hk.gemm_w4a16(x, nib, sc, n, k, None, out_dtype=torch.float32))
+    for r in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), r
+        hk.gemm_w4a16(x, nib, sc, n, k, None, out_dtype=torch.float32)
+        torch.cuda.synchronize()
