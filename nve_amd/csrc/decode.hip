@@ -16,7 +16,6 @@
 #include "common.h"
 #include "act_producer.h"
 #include "w4_launch.h"
-#include "decode_mega.h"
 
 namespace nve {
 
@@ -611,10 +610,6 @@ struct DecodeWs {
   int* arg_i;          // [argmax_slots]
   float* logits;       // [V] (head only, when the caller passes no logits buffer)
   float* part;         // [kMaxAttnSplit][Hq][D + 4] key-split attention partials
-  float* hmid;         // [H] residual after the attention sub-layer (one-kernel layer)
-  unsigned* bar;       // grid-barrier words of the one-kernel layer
-  unsigned long long* trace;  // [512][16] phase timestamps of the one-kernel layer (last in
-                              // the workspace; written only with NVE_DECODE_MEGA_TRACE set)
   size_t bytes;
 };
 
@@ -658,9 +653,6 @@ static DecodeWs layout_ws(const nve_decode_config& c, void* base) {
   w.arg_i = (int*)take((size_t)argmax_slots(c) * 4);
   w.logits = (float*)take((size_t)(c.vocab > 0 ? c.vocab : 1) * 4);
   w.part = (float*)take((size_t)kMaxAttnSplit * c.num_heads * (c.head_dim + 4) * 4);
-  w.hmid = (float*)take((size_t)c.hidden * 4);
-  w.bar = (unsigned*)take(mega_bar_bytes());
-  w.trace = (unsigned long long*)take(512 * 16 * 8);
   w.bytes = off;
   return w;
 }
@@ -789,64 +781,11 @@ static hipError_t gemv_fused(bool w4a8, int src, int pair, const nve::ProdArgs& 
               : launch_w4a16_fused(src, pair, pa, sg, out_dt, K, s, ra);
 }
 
-// The one-kernel layer (decode_mega.hip) where a compiled tiling fits the shapes, with
-// NVE_DECODE_MEGA=1 in the environment (read at every call); by default the five
-// launches, which are faster on MI355X: its grid barriers cost about 3 us each under
-// load (as much as a launch boundary), and the weight loads issued before a barrier
-// delay the barrier's own atomics by about their streaming time.
-static bool decode_mega() {
-  const char* e = getenv("NVE_DECODE_MEGA");
-  return e && e[0] == '1' && e[1] == 0;
-}
-
-static hipError_t mega_layer(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
-                             const DecodeWs& ws, bool w4a8, int cls, int split, hipStream_t s) {
-  nve::mega::Args a{};
-  a.H = c.hidden;
-  a.QD = c.num_heads * c.head_dim;
-  a.KD = c.num_kv_heads * c.head_dim;
-  a.F = c.ffn;
-  a.D = c.head_dim;
-  a.heads = c.num_heads;
-  a.kv_heads = c.num_kv_heads;
-  a.max_seq = c.max_seq;
-  a.xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1;
-  a.eps = c.eps;
-  a.qscale = 1.4426950408889634f / sqrtf((float)c.head_dim);
-  const nve_w4_weight* m[7] = {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down};
-  for (int i = 0; i < 7; ++i) {
-    a.nib[i] = m[i]->nibbles;
-    a.sc[i] = m[i]->scales;
-  }
-  a.norm1 = w.input_norm;
-  a.norm2 = w.post_attn_norm;
-  a.h = io.hidden;
-  a.kc = io.k_cache;
-  a.vc = io.v_cache;
-  a.pos = io.pos;
-  a.rcos = io.rope_cos;
-  a.rsin = io.rope_sin;
-  a.q = ws.q;
-  a.k = ws.k;
-  a.v = ws.v;
-  a.part = ws.part;
-  a.hmid = ws.hmid;
-  a.mid = ws.gate;
-  a.bar = ws.bar;
-  a.trace = getenv("NVE_DECODE_MEGA_TRACE") ? ws.trace : nullptr;
-  return launch_layer_mega(cls, w4a8, split, a, s);
-}
-
 int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                          bool w4a8, hipStream_t s) {
   const DecodeWs ws = layout_ws(c, io.workspace);
   const int H = c.hidden, F = c.ffn, QD = c.num_heads * c.head_dim;
   const bool fuse = decode_fuse();
-  if (fuse && decode_mega()) {
-    const int split = attn_split(c);
-    const int cls = mega_class(c, split);
-    if (cls >= 0) return (int)mega_layer(c, w, io, ws, w4a8, cls, split, s);
-  }
   // attention sub-layer: norm -> Q/K/V (one grouped launch) -> attention -> o_proj (+h)
   {
     const nve_w4_weight qkv[3] = {w.q, w.k, w.v};

@@ -98,19 +98,15 @@ def _run_teacher_forced(torch, m, steps, token0=5, checked=None, record=None):
     return m
 
 
-@pytest.mark.parametrize("fuse,split,mega", [("1", "8", "1"), ("1", "4", "1"), ("1", "2", "1"), ("1", "1", "1"),
-                                             ("1", "8", "0"), ("1", "4", "0"), ("1", "2", "0"), ("1", "1", "0"),
-                                             ("0", "1", "0")])
+@pytest.mark.parametrize("fuse,split", [("1", "8"), ("1", "4"), ("1", "2"), ("1", "1"), ("0", "1")])
 @pytest.mark.parametrize("heads,kv,d", [(4, 2, 64), (6, 2, 128), (8, 1, 64), (2, 2, 256), (24, 8, 128)])
-def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, split, mega, monkeypatch):
-    """Every layer path: the one-kernel layer (NVE_DECODE_MEGA=1, where a compiled tiling
-    fits: here the 4 / 2 / 64 shape), the five launches with producers fused into the
+def test_decode_step_mixed_precision(torch_dev, heads, kv, d, fuse, split, monkeypatch):
+    """Every layer path: the five launches with producers fused into the
     GEMV staging, and standalone RMSNorm / SiLU-mul kernels (NVE_DECODE_FUSE=0); fused
     attention split over 1, 2, 4 or 8 workgroups per head (at 61..66 keys most splits
     have no tile: their partials are empty and must drop out of the merge)."""
     monkeypatch.setenv("NVE_DECODE_FUSE", fuse)
     monkeypatch.setenv("NVE_ATTN_SPLIT", split)
-    monkeypatch.setenv("NVE_DECODE_MEGA", mega)
     m = _model(torch_dev, heads, kv, d)
     _run_teacher_forced(torch_dev, m, steps=6)  # pos 60..65 crosses a 64-key boundary
 
@@ -149,15 +145,13 @@ def test_decode_graph_replay_matches_eager(torch_dev):
     assert int(m.pos.item()) == 40 + n
 
 
-@pytest.mark.parametrize("mega", ["1", "0"])
 @pytest.mark.parametrize("split", ["2", "4", "8"])
-def test_decode_graph_replay_split_attention(torch_dev, split, mega, monkeypatch):
+def test_decode_graph_replay_split_attention(torch_dev, split, monkeypatch):
     """Key-split attention (partials merged in the o_proj staging) under HIP graph
     replay: every replayed token and its logits equal the eager sequence bit for bit,
     with tile counts per split that change as the position crosses tile edges."""
     torch = torch_dev
     monkeypatch.setenv("NVE_ATTN_SPLIT", split)
-    monkeypatch.setenv("NVE_DECODE_MEGA", mega)
     m = _model(torch, 4, 2, 64, layers=2, max_seq=1100, prefill=1020)
     n = 6
     m.start(3)
@@ -175,22 +169,20 @@ def test_decode_graph_replay_split_attention(torch_dev, split, mega, monkeypatch
         assert np.array_equal(m.logits.cpu().numpy(), logits[r]), r
 
 
-@pytest.mark.parametrize("fuse,mega", [("1", "1"), ("1", "0"), ("0", "0")])
-def test_decode_3b_shape_smoke(torch_dev, fuse, mega, monkeypatch):
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_decode_3b_shape_smoke(torch_dev, fuse, monkeypatch):
     """The Llama-3.2-3B shapes (head_dim 128, GQA 3, ffn 8192, vocab 128256) on 2 layers:
-    one teacher-forced step against the oracle over the full logits, for the one-kernel
-    layer, the five launches and the unfused path."""
+    one teacher-forced step against the oracle over the full logits, for the five
+    launches and the unfused path."""
     monkeypatch.setenv("NVE_DECODE_FUSE", fuse)
-    monkeypatch.setenv("NVE_DECODE_MEGA", mega)
     from nve_amd.decode import ModelShape, DecodeModel
     s = ModelShape(layers=2)
     m = DecodeModel(s, max_seq=130, prefill=128, importance=np.array([0.0, 1.0]))
     _run_teacher_forced(torch_dev, m, steps=1)
 
 
-@pytest.mark.parametrize("mega", ["1", "0"])
 @pytest.mark.parametrize("split", ["1", "4", "8"])
-def test_decode_long_cache(torch_dev, split, mega, monkeypatch):
+def test_decode_long_cache(torch_dev, split, monkeypatch):
     """A cache of 8190+ keys: many tiles per workgroup (256 keys per tile at head_dim
     64 -> 32 tiles, 8 per split at 4 splits, 4 at 8), pos 8190..8192 crosses a tile
     edge."""
@@ -277,44 +269,6 @@ def test_decode_bench_model_sampled_layers(torch_dev):
         torch.cuda.synchronize()
         assert int(m.token.item()) == rec[r][0], r
         assert np.array_equal(m.logits.cpu().numpy(), rec[r][1]), r
-
-
-@pytest.mark.parametrize("shape", ["small", "3b"])
-def test_decode_mega_matches_five_launch_layer(torch_dev, shape, monkeypatch):
-    """The one-kernel layer against the five-launch layer on the same state, layer by
-    layer (both precisions): the residual stream and the KV rows agree to the layer
-    tolerance (the f64 norm sums and the attention merge run in a different order), and
-    a second call of the one-kernel layer on the same state is bit-identical to the
-    first (the grid barrier leaves no state behind); the appended key rows agree to one
-    bf16 ulp."""
-    torch = torch_dev
-    from nve_amd.decode import DecodeModel, ModelShape
-    if shape == "small":
-        m = _model(torch, 4, 2, 64, layers=2, importance=(0.0, 1.0), max_seq=600, prefill=520)
-    else:
-        m = DecodeModel(ModelShape(layers=2), max_seq=1024, prefill=512, importance=np.array([0.0, 1.0]))
-    m.start(3)
-    m._advance(1)
-    for li in range(m.shape.layers):
-        st = (m.hidden.clone(), m.layers[li]["k_cache"].clone(), m.layers[li]["v_cache"].clone())
-        outs = []
-        for mega in ("0", "1", "1"):
-            monkeypatch.setenv("NVE_DECODE_MEGA", mega)
-            m.hidden.copy_(st[0])
-            m.layers[li]["k_cache"].copy_(st[1])
-            m.layers[li]["v_cache"].copy_(st[2])
-            m.layer(li)
-            torch.cuda.synchronize()
-            outs.append((m.hidden.clone(), m.layers[li]["k_cache"].clone()))
-        five, mega1, mega2 = outs
-        h_in = st[0].cpu().numpy()
-        err = rel_err_norm(mega1[0].cpu().numpy() - h_in, five[0].cpu().numpy() - h_in)
-        print(f"layer {li} w4a8={m.use_w4a8[li]}: one-kernel vs five-launch {err:.2e}", flush=True)
-        assert err <= TOL_LAYER, (li, err)
-        assert torch.equal(mega1[0], mega2[0]) and torch.equal(mega1[1], mega2[1])
-        pos = m.prefill
-        ka, kb = mega1[1][:, pos].float(), five[1][:, pos].float()
-        assert torch.allclose(ka, kb, rtol=2.0 ** -7, atol=TOL_LAYER * float(kb.pow(2).mean().sqrt()))
 
 
 @pytest.mark.parametrize("lm8", [True, False])
