@@ -366,6 +366,10 @@ int nve_hip_last_status(void);
 const char *nve_hip_status_string(int status);
 /* Library version string. */
 const char *nve_hip_version(void);
+/* Hash of the sources and compile flags the library was built from (32 hex digits;
+ * no reference counterpart).  A loader compares it with the hash of the sources it
+ * ships with and refuses a library built from other sources. */
+const char *nve_hip_build_id(void);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,7 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_last_status": (_i, []),
     "nve_hip_status_string": (C.c_char_p, [_i]),
     "nve_hip_version": (C.c_char_p, []),
+    "nve_hip_build_id": (C.c_char_p, []),
 }
 
 
@@ -125,6 +126,13 @@ def lib() -> C.CDLL:
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        from .build_ext import source_id
+        built, tree = L.nve_hip_build_id().decode(), source_id()
+        if built != tree:
+            raise RuntimeError(
+                f"{LIB_PATH} was built from other sources (build id {built}, sources {tree}); "
+                "rebuild it: `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
         _lib = L
     return _lib
 

@@ -6,6 +6,7 @@ The library is compiled from nve_amd/csrc/*.hip: one hipcc job per translation u
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -35,9 +36,27 @@ CFLAGS = [
 ]
 
 
-def _compile(src: Path) -> Path:
+INCLUDE = PKG.parent / "include"
+
+
+def source_id() -> str:
+    """Hash of everything the library is built from: every file under csrc/ and
+    include/ (name and bytes, in sorted order) and the compile flags.  The build embeds
+    it (nve_hip_build_id), and the loader refuses a library whose id differs from the
+    tree's, so a stale prebuilt .so can never be what runs."""
+    h = hashlib.sha256()
+    h.update(" ".join(CFLAGS).encode())
+    for d in (CSRC, INCLUDE):
+        for f in sorted(p for p in d.iterdir() if p.is_file() and p.suffix in (".hip", ".h", ".cpp")):
+            h.update(f"{d.name}/{f.name}\0".encode())
+            h.update(f.read_bytes())
+            h.update(b"\0")
+    return h.hexdigest()[:32]
+
+
+def _compile(src: Path, build_id: str) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, f'-DNVE_BUILD_ID="{build_id}"', "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
@@ -50,8 +69,9 @@ def build(verbose: bool = True) -> Path:
     OBJ.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
+    bid = source_id()
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda f: _compile(f, bid), srcs))
     tmp = LIB.with_suffix(".so.tmp")
     # hipBLASLt: the dense GEMM of the large-M prefill path (gemm_blas.hip)
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-lhipblaslt", "-o", str(tmp)]

@@ -100,6 +100,11 @@ int nve_hip_last_status(void) { return g_last_status; }
 
 const char* nve_hip_version(void) { return "nve_hip 0.1.0 gfx950"; }
 
+#ifndef NVE_BUILD_ID
+#error "NVE_BUILD_ID must be defined by the build (hash of the sources it compiles)"
+#endif
+const char* nve_hip_build_id(void) { return NVE_BUILD_ID; }
+
 // ---- activation quantization --------------------------------------------------
 int nve_hip_quantize_q8(const void* x, int x_dtype, int M, int K, int8_t* xq, float* scales,
                         void* stream) {

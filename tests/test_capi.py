@@ -151,3 +151,25 @@ def test_product_path_has_no_oracle_dependency():
     for p in (ROOT / "nve_amd").rglob("*"):
         if p.suffix in (".py", ".hip", ".h", ".cpp"):
             assert "oracle" not in p.read_text(), p
+
+
+def test_build_id_matches_sources(L):
+    """The loaded library was built from the sources in this tree (the loader refuses
+    any other, so tests and the bench never measure a stale binary)."""
+    from nve_amd.build_ext import source_id
+    bid = L.nve_hip_build_id().decode()
+    assert len(bid) == 32 and bid == source_id()
+
+
+def test_build_id_changes_with_sources(tmp_path, monkeypatch):
+    from nve_amd import build_ext
+    a = build_ext.source_id()
+    d = tmp_path / "csrc"
+    d.mkdir()
+    for f in build_ext.CSRC.iterdir():
+        if f.is_file():
+            (d / f.name).write_bytes(f.read_bytes())
+    monkeypatch.setattr(build_ext, "CSRC", d)
+    assert build_ext.source_id() == a
+    (d / "common.h").write_bytes((d / "common.h").read_bytes() + b"\n")
+    assert build_ext.source_id() != a
