@@ -443,6 +443,51 @@ def stream_probe(torch, L) -> float:
     return buf_gbs(2 << 30, ms)
 
 
+def same_size_read(torch, L, nbytes: int, copies: int, launches_per_graph: int = 40) -> dict:
+    """The streaming-read ceiling at one byte count: the library's read probe
+    (nve_hip_stream_read_mode) over `copies` rotating buffers of `nbytes` each -- the
+    same rotation the GEMV table uses for that shape, so the MALL serves neither more
+    nor less -- timed like the GEMVs (a graph of back-to-back launches, HIP events on
+    the replay stream).  Every probe form (one-shot, grid-stride at 1 and 2 workgroups
+    per CU) is timed; the fastest is the ceiling."""
+    stride = (nbytes + 4095) // 4096 * 4096
+    n16 = (nbytes + 15) // 16 * 16
+    buf = torch.empty(stride * copies, dtype=torch.uint8, device="cuda")
+    buf.fill_(0x5A)
+    sink = torch.zeros(1024, device="cuda")
+    best = None
+    for mode in (0, 1, 2):
+        def body(mode=mode):
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(launches_per_graph):
+                assert L.nve_hip_stream_read_mode(buf.data_ptr() + (i % copies) * stride, n16, sink.data_ptr(),
+                                                  mode, s) == 0
+        body()
+        g = capture(torch, body)
+        time_graphs(torch, [g], 2)
+        us = time_graphs(torch, [g], 10) * 1e3 / launches_per_graph
+        if best is None or us < best["us"]:
+            best = {"us": round(us, 3), "GBs": round(nbytes / us / 1e3, 1),
+                    "form": ("one-shot", "grid-stride 1 wg/CU", "grid-stride 2 wg/CU")[mode]}
+    del buf, g
+    return best
+
+
+def add_read_ceiling(torch, L, table: dict, copies_of) -> dict:
+    """Annotate every row of a kernel table with the same-size read ceiling:
+    read_us and frac_of_same_size_read = read_us / us (1.0 = the GEMV streams its
+    bytes as fast as a pure read of the same size)."""
+    cache = {}
+    for key, row in table.items():
+        c = copies_of(key)
+        if (row["bytes"], c) not in cache:
+            cache[(row["bytes"], c)] = same_size_read(torch, L, row["bytes"], c)
+        r = cache[(row["bytes"], c)]
+        row["read_us"] = r["us"]
+        row["frac_of_same_size_read"] = round(r["us"] / row["us"], 4)
+    return {str(b): {"copies": c, **r} for (b, c), r in sorted(cache.items())}
+
+
 def buf_gbs(nbytes, ms):
     return nbytes / (ms * 1e-3) / 1e9
 
@@ -827,8 +872,14 @@ def main():
     value = sb / (ms * 1e-3) / 1e9
     log(f"step: {ms * 1e3:.1f} us, {sb / 1e6:.1f} MB algorithmic, {value:.1f} GB/s")
 
+    log("same-size read ceilings (8B rows):")
+    read_8b = add_read_ceiling(torch, L, table, lambda key: copies_head if key.startswith("lm_head") else copies_layer)
+    for b, r in read_8b.items():
+        log(f"  {int(b) / 1e6:8.2f} MB  {r['us']:8.2f} us {r['GBs']:8.1f} GB/s ({r['form']})")
     log("the step's lm_head launches:")
     heads = step_head_kernels(torch, step)
+    for h in heads.values():
+        h["read_us"] = same_size_read(torch, L, h["bytes"], copies_head)["us"]
     log("batched W4A8 sweep (per-token int8 activations):")
     sweep = batched_sweep(torch, L, weights)
     stream_gbs = stream_probe(torch, L)
@@ -852,6 +903,7 @@ def main():
         acts1b[nm + "16"] = x.to(torch.float16)
         acts1b[nm + "b"] = x.to(torch.bfloat16)
     table_1b = kernel_table(torch, L, w1b, acts1b, suite=SUITE_1B)
+    read_1b = add_read_ceiling(torch, L, table_1b, lambda key: 16)
     del w1b, acts1b
     torch.cuda.empty_cache()
     decode = None if args.no_decode else decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens,
@@ -884,6 +936,7 @@ def main():
         return {"kernel": kernels[label], "bound": "hbm", "achieved": h["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(h["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic.get(label),
                 "achievable_peak": round(stream_gbs, 1), "frac_of_achievable": round(h["GBs"] / stream_gbs, 4),
+                "same_size_read_us": h["read_us"], "frac_of_same_size_read": round(h["read_us"] / h["us"], 4),
                 "bytes_per_launch": h["bytes"], "us_per_launch": h["us"]}
 
     rec = {
@@ -916,6 +969,8 @@ def main():
                                    "w4a16_all": agg("w4a16", [n for n, _, _ in SUITE_8B])},
         "suite_1b": table_1b,
         "hbm_stream_probe_GBs": round(stream_gbs, 1),
+        "same_size_read_8b": read_8b,
+        "same_size_read_1b": read_1b,
         "batched_w4a8_8b": sweep,
         "decode_3b": decode,
         "decode_3b_long_context": decode_long,

@@ -354,6 +354,30 @@ int nve_hip_layer_forward_decode_noalloc(const nve_decode_config *cfg, const nve
  * token into hidden, *pos += 1. */
 int nve_hip_decode_head(const nve_decode_config *cfg, const nve_decode_head *head, int use_w4a8,
                         void *stream);
+/* Diagnostic: one fused launch of the layer, issued exactly as
+ * nve_hip_layer_forward_decode issues it (same kernels, arguments and workspace), with
+ * its input and output exposed so that each fused producer and epilogue can be checked
+ * on its own (no reference counterpart; the tests use it).  io->workspace is required.
+ *   NVE_STAGE_QKV      RMSNorm(io->hidden) -> grouped Q/K/V GEMV -> RoPE: out = q
+ *                      rotated and scaled by log2(e)/sqrt(D) (f32 [heads * D]); the new
+ *                      key (rotated) and value rows go to the caches at *io->pos (bf16).
+ *   NVE_STAGE_O_MERGE  in = key-split attention partials, f32 [split][heads][D + 4]
+ *                      records (m, l, -, -, acc[D]), merged in the o_proj staging;
+ *                      io->hidden += o_proj(merged).  split =
+ *                      nve_hip_decode_attn_splits(cfg); NVE_ERR_SHAPE when it is 1.
+ *   NVE_STAGE_GATE_UP  RMSNorm(io->hidden) -> gate/up pair -> out = silu(gate) * up,
+ *                      fp16 [ffn].
+ *   NVE_STAGE_DOWN     in = fp16 [ffn] -> down GEMV; io->hidden += y.
+ * in / out 16-byte aligned. */
+#define NVE_STAGE_QKV 0
+#define NVE_STAGE_O_MERGE 1
+#define NVE_STAGE_GATE_UP 2
+#define NVE_STAGE_DOWN 3
+int nve_hip_decode_stage(const nve_decode_config *cfg, const nve_layer_weights *w, const nve_decode_io *io,
+                         int use_w4a8, int stage, const void *in, void *out, void *stream);
+/* Key splits the layer's attention uses for cfg (1, 2, 4 or 8; NVE_ATTN_SPLIT in the
+ * environment overrides, as for the layer). */
+int nve_hip_decode_attn_splits(const nve_decode_config *cfg);
 /* hidden = embed[*token] (bf16 -> fp32). */
 int nve_hip_embed(const uint16_t *embed, const int *token, float *hidden, int hidden_size,
                   void *stream);
@@ -362,6 +386,10 @@ int nve_hip_embed(const uint16_t *embed, const int *token, float *hidden, int hi
 /* Read-only HBM streaming probe: reads `bytes` (multiple of 16, 16-byte aligned)
  * from buf and writes one f32 per workgroup-slot into sink[0..1023]. */
 int nve_hip_stream_read(const void *buf, size_t bytes, float *sink, void *stream);
+/* The same probe in a chosen form: mode 0 = one-shot (as nve_hip_stream_read: one
+ * wave per 8 KiB), mode 1 / 2 = grid-stride over 1 / 2 workgroups per CU.  The bench
+ * takes the faster form at each byte count as the same-size read ceiling. */
+int nve_hip_stream_read_mode(const void *buf, size_t bytes, float *sink, int mode, void *stream);
 int nve_hip_last_status(void);
 const char *nve_hip_status_string(int status);
 /* Library version string. */

@@ -22,6 +22,7 @@ XS_GROUP32_F32, XS_ROW_BF16 = 0, 1
 MAX_K = 32768
 GEMV_AUTO, GEMV_ONESHOT, GEMV_PERSISTENT = 0, 1, 2
 MAX_M = 16
+STAGE_QKV, STAGE_O_MERGE, STAGE_GATE_UP, STAGE_DOWN = 0, 1, 2, 3
 
 _p = C.c_void_p
 _i = C.c_int
@@ -54,10 +55,13 @@ SIGNATURES: dict[str, tuple] = {
     "nve_dequant_w4a16": (None, [_p, _p, _p, _p, _i, _i, _p]),
     "nve_use_w4a8": (_i, [C.c_double]),
     "nve_hip_stream_read": (_i, [_p, C.c_size_t, _p, _p]),
+    "nve_hip_stream_read_mode": (_i, [_p, C.c_size_t, _p, _i, _p]),
     "nve_hip_set_gemv_policy": (_i, [_i, _i, _i]),
     "nve_hip_decode_workspace_bytes": (C.c_size_t, [_p]),
     "nve_hip_layer_forward_decode": (_i, [_p, _p, _p, _i, _p]),
     "nve_hip_layer_forward_decode_noalloc": (_i, [_p, _p, _p, _i, _p]),
+    "nve_hip_decode_stage": (_i, [_p, _p, _p, _i, _i, _p, _p, _p]),
+    "nve_hip_decode_attn_splits": (_i, [_p]),
     "nve_hip_decode_head": (_i, [_p, _p, _i, _p]),
     "nve_hip_embed": (_i, [_p, _p, _p, _i, _p]),
     "nve_hip_last_status": (_i, []),

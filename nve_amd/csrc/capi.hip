@@ -65,7 +65,7 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
                                 hipStream_t s);
 hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, float* scales,
                             hipStream_t stream);
-hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream);
+hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, int mode, hipStream_t stream);
 hipError_t launch_w4a8_unaligned(const int8_t* xq, const float* xs, const uint8_t* nib, const float* ws, void* out,
                                  int out_dt, int N, int K, hipStream_t s);
 hipError_t launch_w4a16_unaligned(const void* x, int x_dt, const uint8_t* nib, const float* sc, const float* awq,
@@ -457,6 +457,25 @@ int nve_hip_layer_forward_decode_noalloc(const nve_decode_config* cfg, const nve
   return set_status(layer_forward_decode_noalloc(*cfg, *w, *io, use_w4a8 != 0, (hipStream_t)stream));
 }
 
+int nve_hip_decode_stage(const nve_decode_config* cfg, const nve_layer_weights* w, const nve_decode_io* io,
+                         int use_w4a8, int stage, const void* in, void* out, void* stream) {
+  const int st = check_layer_args(cfg, w, io, true);
+  if (st != NVE_OK) return set_status(st);
+  if (stage < NVE_STAGE_QKV || stage > NVE_STAGE_DOWN) return set_status(NVE_ERR_DTYPE);
+  const bool need_in = stage == NVE_STAGE_O_MERGE || stage == NVE_STAGE_DOWN;
+  const bool need_out = stage == NVE_STAGE_QKV || stage == NVE_STAGE_GATE_UP;
+  if ((need_in && !in) || (need_out && !out)) return set_status(NVE_ERR_NULL);
+  if ((in && !aligned(in, 16)) || (out && !aligned(out, 16))) return set_status(NVE_ERR_ALIGN);
+  return set_status(decode_stage(*cfg, *w, *io, use_w4a8 != 0, stage, in, out, (hipStream_t)stream));
+}
+
+int nve_hip_decode_attn_splits(const nve_decode_config* cfg) {
+  if (!cfg) return set_status(NVE_ERR_NULL);
+  const int st = check_decode(*cfg);
+  if (st != NVE_OK) return set_status(st);
+  return attn_splits(*cfg);  // a count, not a status
+}
+
 int nve_hip_decode_head(const nve_decode_config* cfg, const nve_decode_head* hd, int use_w4a8, void* stream) {
   if (!cfg || !hd) return set_status(NVE_ERR_NULL);
   int st = check_decode(*cfg);
@@ -490,7 +509,15 @@ int nve_hip_stream_read(const void* buf, size_t bytes, float* sink, void* stream
   if (!buf || !sink) return set_status(NVE_ERR_NULL);
   if (bytes == 0 || bytes % 16 != 0) return set_status(NVE_ERR_SHAPE);
   if (!aligned(buf, 16) || !aligned(sink, 4)) return set_status(NVE_ERR_ALIGN);
-  return from_hip(launch_stream_read(buf, bytes, sink, (hipStream_t)stream));
+  return from_hip(launch_stream_read(buf, bytes, sink, 0, (hipStream_t)stream));
+}
+
+int nve_hip_stream_read_mode(const void* buf, size_t bytes, float* sink, int mode, void* stream) {
+  if (!buf || !sink) return set_status(NVE_ERR_NULL);
+  if (bytes == 0 || bytes % 16 != 0) return set_status(NVE_ERR_SHAPE);
+  if (mode < 0 || mode > 2) return set_status(NVE_ERR_DTYPE);
+  if (!aligned(buf, 16) || !aligned(sink, 4)) return set_status(NVE_ERR_ALIGN);
+  return from_hip(launch_stream_read(buf, bytes, sink, mode, (hipStream_t)stream));
 }
 
 // ---- drop-in launchers (reference names and argument order) ----------------------

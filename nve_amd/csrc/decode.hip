@@ -846,6 +846,57 @@ int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w,
   return NVE_OK;
 }
 
+// One fused launch of the decode layer, exactly as layer_forward_decode issues it (same
+// kernel instantiation, arguments and workspace), with its input / output exposed:
+//   STAGE_QKV:    RMSNorm(h) -> Q/K/V GEMV -> RoPE; q (scaled) to out f32 [Hq*D], the new
+//                 key / value rows to the caches at *pos.
+//   STAGE_O_MERGE: attention partials in (f32 [split][Hq][D+4]) merged in the o_proj
+//                 staging; h += o_proj(merged).  split = the layer's key-split count.
+//   STAGE_GATE_UP: RMSNorm(h) -> gate/up GEMV pair -> silu(gate) * up, fp16 out [F].
+//   STAGE_DOWN:   fp16 in [F] -> down GEMV (W4A8: quantized in its staging); h += y.
+int decode_stage(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io, bool w4a8,
+                 int stage, const void* in, void* out, hipStream_t s) {
+  const DecodeWs ws = layout_ws(c, io.workspace);
+  const int H = c.hidden, F = c.ffn, QD = c.num_heads * c.head_dim;
+  switch (stage) {
+    case NVE_STAGE_QKV: {
+      const nve_w4_weight qkv[3] = {w.q, w.k, w.v};
+      void* outs[3] = {out, ws.k, ws.v};
+      const nve::EpiArgs ra{(float*)out, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.max_seq,
+                             c.head_dim / 2, 1.4426950408889634f / sqrtf((float)c.head_dim)};
+      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_ROPE, nve::ProdArgs{io.hidden, w.input_norm, c.eps},
+                         segs3(qkv, outs, 3), NVE_DT_F32, H, s, ra));
+      return NVE_OK;
+    }
+    case NVE_STAGE_O_MERGE: {
+      const int split = attn_split(c);
+      if (split < 2) return NVE_ERR_SHAPE;  // no partials to merge: o_proj is the plain GEMV
+      NVE_TRY(gemv_fused(w4a8, split == 8 ? nve::SRC_ATTN8 : (split == 4 ? nve::SRC_ATTN4 : nve::SRC_ATTN2),
+                         nve::PAIR_NONE, nve::ProdArgs{in, nullptr, 0.0f, c.head_dim, c.num_heads},
+                         one_seg(w.o, io.hidden), NVE_DT_F32_ACCUM, QD, s));
+      return NVE_OK;
+    }
+    case NVE_STAGE_GATE_UP: {
+      const nve_w4_weight gu[2] = {w.gate, w.up};
+      void* outs[2] = {out, nullptr};
+      NVE_TRY(gemv_fused(w4a8, nve::SRC_NORM, nve::PAIR_SWIGLU, nve::ProdArgs{io.hidden, w.post_attn_norm, c.eps},
+                         segs3(gu, outs, 2), NVE_DT_F16, H, s));
+      return NVE_OK;
+    }
+    case NVE_STAGE_DOWN:
+      if (w4a8)
+        NVE_TRY(gemv_fused(true, nve::SRC_F16, nve::PAIR_NONE, nve::ProdArgs{in, nullptr, 0.0f},
+                           one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
+      else
+        NVE_TRY(launch_w4a16(in, NVE_DT_F16, one_seg(w.down, io.hidden), NVE_DT_F32_ACCUM, F, s));
+      return NVE_OK;
+    default:
+      return NVE_ERR_DTYPE;
+  }
+}
+
+int attn_splits(const nve_decode_config& c) { return attn_split(c); }
+
 int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8, hipStream_t s) {
   const DecodeWs ws = layout_ws(c, hd.workspace);
   float* logits = hd.logits ? hd.logits : ws.logits;

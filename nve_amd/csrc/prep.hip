@@ -265,6 +265,29 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
   if (a == 0x12345678u) sink[blockIdx.x & 1023] = 1.0f;
 }
 
+// Grid-stride form of the same probe: a fixed grid (one or two workgroups per CU)
+// whose waves each read 8 x 1 KiB per iteration, stepping by the grid's span until
+// the buffer is covered.  Fewer, longer-lived waves than the one-shot form: the better
+// of the two at large sizes.
+__global__ __launch_bounds__(256) void stream_read_gs_kernel(const uint4* __restrict__ buf, size_t n16,
+                                                             float* __restrict__ sink) {
+  const size_t nwaves = (size_t)gridDim.x * 4;
+  const int lane = threadIdx.x & 63;
+  uint32_t a = 0;
+  for (size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6); wave * 512 < n16; wave += nwaves) {
+    uint4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      size_t i = (wave * 8 + j) * 64 + lane;
+      if (i >= n16) i = n16 - 1;
+      v[j] = ld_stream(buf + i);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  if (a == 0x12345678u) sink[blockIdx.x & 1023] = 1.0f;
+}
+
 // ---- W4 dequantization (prefill path) ---------------------------------------
 // _nve_dequant_w4a16 (cuda/nve_kernels.cu:397-433): w[n, k] = f32(nibble - 8) * scale,
 // times awq[k] when given (a second f32 rounding, as QuantizedTensor::to_f32_vec does
@@ -402,10 +425,17 @@ hipError_t launch_q4_repack(const uint8_t* q4, size_t nblocks, uint8_t* nib, flo
   return hipGetLastError();
 }
 
-hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, hipStream_t stream) {
+hipError_t launch_stream_read(const void* buf, size_t bytes, float* sink, int mode, hipStream_t stream) {
   const size_t n16 = bytes / 16;
   const size_t grid = (n16 + 2047) / 2048;  // 4 waves x 8 spans x 64 lanes per workgroup
-  hipLaunchKernelGGL(nve::stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, stream, (const uint4*)buf, n16, sink);
+  if (mode == 0) {
+    hipLaunchKernelGGL(nve::stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, stream, (const uint4*)buf, n16,
+                       sink);
+  } else {
+    const size_t gs = (size_t)256 * mode;  // mode = workgroups per CU of the 256-CU MI355X
+    hipLaunchKernelGGL(nve::stream_read_gs_kernel, dim3((unsigned)(grid < gs ? grid : gs)), dim3(256), 0, stream,
+                       (const uint4*)buf, n16, sink);
+  }
   return hipGetLastError();
 }
 

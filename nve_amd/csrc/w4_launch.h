@@ -184,6 +184,9 @@ int check_decode(const nve_decode_config& c);
 int layer_forward_decode(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                          bool w4a8, hipStream_t s);
 int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8, hipStream_t s);
+int decode_stage(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io, bool w4a8,
+                 int stage, const void* in, void* out, hipStream_t s);
+int attn_splits(const nve_decode_config& c);
 int layer_forward_decode_noalloc(const nve_decode_config& c, const nve_layer_weights& w, const nve_decode_io& io,
                                  bool w4a8, hipStream_t s);
 // Fused-producer GEMVs (act_producer.h).

@@ -207,10 +207,10 @@ def test_w4a8_grouped_exact(orc, env, ns, k, mode):
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("xs_mode", ["group_f32", "row_bf16"])
 def test_w4a8_batched_exact(orc, env, n, k, m, xs_mode):
-    """Batched W4A8: M = 1 on the one-row GEMV, M = 2 on the staged v_dot4 kernel (the
-    shapes here all fit its LDS), M >= 3 on int8 MFMA (with the -8 correction MFMA: the
-    LDS-ring kernel where K % 128 == 0 and each wave has a full ring of quads, else the
-    register kernel);
+    """Batched W4A8: M = 1 on the one-row GEMV; M >= 2 on the LDS-ring int8 MFMA kernel
+    (with the -8 correction MFMA) where K % 128 == 0 and each wave has a full ring of
+    quads; otherwise M = 2 on the staged v_dot4 kernel (the shapes here all fit its LDS)
+    and M >= 3 on the register MFMA kernel;
     every row of every activation exact.  Row mode: one power-of-two bf16 scale per
     activation row (bf16 2^e is exact)."""
     torch, hk, L, pol = env
