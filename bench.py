@@ -635,7 +635,8 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     vendor BLAS -- as GpuWeight::matmul_x does with candle, src/gpu_layer.rs:219-237).
     Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time.
     library_us: nve_hip_gemm_w4a16_ws with its workspace (dequant + hipBLASLt from
-    M = 512 on, the fused kernels below)."""
+    M = 512 on, the fused kernels below), fp32 output; library_f16_out_us: the same
+    with fp16 output, the output type of the reference-method timing."""
     g = torch.Generator(device="cuda").manual_seed(17)
     n, k = 14336, 4096
     nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
@@ -665,16 +666,19 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
         wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
         ws = torch.empty(wsb, dtype=torch.uint8, device="cuda") if wsb else None
         us_lib = timed(lambda: hk.gemm_w4a16_ws(x, nib, sc, n, k, ws))
+        # fp16 output, as torch.matmul writes in the reference-method timing above
+        us_lib16 = timed(lambda: hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16))
         fl = 2.0 * m * n * k
         out["rows"].append({"M": m, "fused_us": round(us, 1), "fused_TFLOPs": round(fl / us / 1e6, 1),
                             "frac_mfma_peak": round(fl / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
                             "dequant_plus_blas_us": round(us_ref, 1),
                             "library_us": round(us_lib, 1),
+                            "library_f16_out_us": round(us_lib16, 1),
                             # the library's rule (gemm_blas.hip): dequant + hipBLASLt from M = 512
                             # with a workspace; below it the workspace holds K-split partials
                             "library_path": "dequant + hipBLASLt" if m >= 512 and wsb else "fused"})
         log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us, "
-            f"nve_hip_gemm_w4a16_ws {us_lib:.1f} us")
+            f"nve_hip_gemm_w4a16_ws {us_lib:.1f} us (fp16 out {us_lib16:.1f} us)")
         del x, wf, ws
     return out
 

@@ -229,10 +229,10 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * in fp32 on MFMA (M <= 320: weight-streaming kernels, where K % 128 == 0 and N <= 16384 an
  * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; larger M: LDS-tiled).  x [M, K]
  * row-major F16/BF16 (16-byte aligned); awq [K] or NULL; out [M, N] row-major F16,
- * BF16 or F32.  K % 64 == 0.  With F32 output and a tile grid too small to fill the
- * GPU, K is split over workgroups whose fp32 partials are added atomically: the last
- * bits of such an output may differ from call to call (nve_hip_gemm_w4a16_ws with its
- * workspace is bit-reproducible). */
+ * BF16 or F32.  K % 64 == 0.  Bit-reproducible: the same inputs give the same bits on
+ * every call (no atomic accumulation; nve_hip_gemm_w4a16_ws can also split K over
+ * workgroups for small tile grids, with its fp32 partials in the workspace, added in a
+ * fixed order). */
 int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles, const float *scales,
                        const float *awq, void *out, int out_dtype, int N, int K, void *stream);
 

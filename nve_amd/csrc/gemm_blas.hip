@@ -34,7 +34,8 @@ namespace {
 
 constexpr int kGemmBlasMinM = 512;        // from here on dequant + GEMM is faster
 constexpr size_t kBlasWorkspace = 32u << 20;
-constexpr int kBlasCandidates = 8;  // heuristic candidates timed on the first call per shape
+constexpr int kBlasCandidates = 32;  // heuristic candidates timed on the first call per shape
+constexpr int kBlasTimedRuns = 5;    // timed runs per candidate (after one untimed run)
 
 size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -75,7 +76,8 @@ bool make_descs(Descs& ds, int M, int N, int K, int x_dt, int out_dt) {
          hipblasLtMatrixLayoutCreate(&ds.d, blas_type(out_dt), N, M, N) == HIPBLAS_STATUS_SUCCESS;
 }
 
-// Heuristic candidates for the shape, each timed (3 runs) on the caller's stream; only
+// Heuristic candidates for the shape, each timed (kBlasTimedRuns runs after one untimed
+// run) on the caller's stream; only
 // a candidate in the success state, within the workspace limit, whose runs all
 // returned success can be chosen.  ok == false when none qualifies (or no candidate
 // exists).  A single candidate is still run once to check it.  `out` and the
@@ -115,7 +117,7 @@ AlgoChoice select_algo(hipblasLtHandle_t h, const Descs& ds, const void* x, void
     bool run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d, &res[c].algo,
                                   bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
     hipEventRecord(e0, s);
-    for (int r = 0; run_ok && r < 3; ++r)
+    for (int r = 0; run_ok && r < kBlasTimedRuns; ++r)
       run_ok = hipblasLtMatmul(h, ds.op, &alpha, ws, ds.a, x, ds.b, &beta, out, ds.d, out, ds.d, &res[c].algo,
                                bws, kBlasWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
     hipEventRecord(e1, s);

@@ -135,12 +135,10 @@ __device__ __forceinline__ void gemm_mfma(const uint16_t* sX, const uint16_t* sW
 }
 
 // SPLIT: the K range is divided over gridDim.z workgroups per output tile (launches
-// whose tile grid alone would leave most CUs idle: small M).  SPLIT_ATOMIC: the
-// workgroups add their fp32 partial sums into a zeroed fp32 output (the order of the
-// additions varies from run to run); SPLIT_PARTS: workgroup z stores its partial
-// tile to out + z * M * N and split_reduce_kernel adds the partials in the order
-// z = 0, 1, ... (bit-reproducible).
-enum { SPLIT_NONE = 0, SPLIT_ATOMIC = 1, SPLIT_PARTS = 2 };
+// whose tile grid alone would leave most CUs idle: small M).  SPLIT_PARTS: workgroup z
+// stores its partial tile to out + z * M * N and split_reduce_kernel adds the partials
+// in the order z = 0, 1, ... (bit-reproducible; no atomic accumulation anywhere).
+enum { SPLIT_NONE = 0, SPLIT_PARTS = 2 };
 template <bool BF16, bool AWQ, int OUT_DT, int SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_w4a16_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ nib, const float* __restrict__ scales,
@@ -201,9 +199,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < M && n < N) {
-          if (SPLIT == SPLIT_ATOMIC)
-            atomicAdd((float*)out + (size_t)m * N + n, acc[i][j][r]);
-          else if (SPLIT == SPLIT_PARTS)
+          if (SPLIT == SPLIT_PARTS)
             ((float*)out)[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = acc[i][j][r];
           else
             store_out<OUT_DT>(out, (size_t)m * N + n, acc[i][j][r]);
@@ -626,11 +622,6 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   out[i] = y;
 }
 
-__global__ __launch_bounds__(256) void zero_f32_kernel(float4* __restrict__ p, size_t n4) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n4) p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-}
-
 #undef GEMM_ISSUE
 #undef GEMM_STAGE
 
@@ -658,9 +649,9 @@ size_t gemm_split_parts_bytes(int M, int N, int K) {
   return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
 }
 
-// parts: NULL -> a split launch adds its partials atomically into a zeroed output;
-// else (parts_bytes >= gemm_split_parts_bytes) the partials go to `parts` and are added
-// in a fixed order.
+// parts (parts_bytes >= gemm_split_parts_bytes): a split launch stores its partials
+// there and adds them in a fixed order; without them the product is not split, so every
+// call gives the same bits.
 template <bool BF16, bool AWQ>
 static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
                                 void* out, int out_dt, int N, int K, float* parts, size_t parts_bytes,
@@ -669,31 +660,17 @@ static hipError_t launch_gemm_t(const void* x, int M, const uint8_t* nib, const 
   int split = gemm_split(M, N, K, out_dt);
   const int kit = K / nve::GM_BK;
   const size_t n = (size_t)M * N;
-  bool use_parts = false;
-  if (split > 1 && parts) {
-    if (parts_bytes >= (size_t)split * n * sizeof(float))
-      use_parts = true;
-    else
-      split = 1;  // a workspace too small for the partials: no split (still reproducible)
-  } else if (split > 1) {
-    // M * N * 4 bytes zeroed with float4 stores when possible
-    if (n % 4 == 0 && ((uintptr_t)out & 15) == 0) {
-      hipLaunchKernelGGL(nve::zero_f32_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, (float4*)out, n / 4);
-    } else {
-      split = 1;
-    }
-  }
+  if (split > 1 && !(parts && parts_bytes >= (size_t)split * n * sizeof(float)))
+    split = 1;  // no room for the partials: one pass over K
   const int k_split = ((kit + split - 1) / split) * nve::GM_BK;
   const dim3 grid(tn, tm, split);
 #define NVE_GEMM(OD, SP, O)                                                                                    \
   hipLaunchKernelGGL((nve::gemm_w4a16_kernel<BF16, AWQ, OD, SP>), grid, dim3(256), 0, s, (const uint16_t*)x, nib, \
                      sc, awq, O, M, N, K, k_split)
-  if (split > 1 && use_parts) {
+  if (split > 1) {
     NVE_GEMM(NVE_DT_F32, nve::SPLIT_PARTS, (void*)parts);
     hipLaunchKernelGGL(nve::split_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, parts,
                        (float*)out, n, split);
-  } else if (split > 1) {
-    NVE_GEMM(NVE_DT_F32, nve::SPLIT_ATOMIC, out);
   } else {
     switch (out_dt) {
       case NVE_DT_F16: NVE_GEMM(NVE_DT_F16, nve::SPLIT_NONE, out); break;

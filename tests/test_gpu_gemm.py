@@ -167,8 +167,8 @@ def test_gemm_w4a16_ws_blas_path(orc, torch_dev, hk, m, n, k, xdt, with_awq):
 
 def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
     """Below M = 512, or without a workspace, nve_hip_gemm_w4a16_ws is the fused kernel
-    (compared at fp16 output: fp32 output at small M splits K with atomic adds, whose
-    order is not fixed)."""
+    (compared at fp16 output: with a workspace an fp32 product at small M splits K, whose
+    partials then add in a different order than one pass)."""
     torch = torch_dev
     # below M = 512 the workspace holds only K-split partials (none for M <= 16)
     assert hk.gemm_w4a16_workspace_bytes(16, 256, 1024) == 0
@@ -221,8 +221,8 @@ def test_gemm_w4a16_ws_graph_capture(orc, torch_dev, hk):
 def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
     """With a workspace, a K-split fp32 product stores its partials there and adds them
     in a fixed order: every call -- eager or replayed from a HIP graph -- gives the same
-    bits, within the W4A16 bar of the oracle and within fp32 rounding of the atomic
-    split of nve_hip_gemm_w4a16."""
+    bits, within the W4A16 bar of the oracle and within fp32 rounding of the unsplit
+    product of nve_hip_gemm_w4a16 (which is itself the same on every call)."""
     torch = torch_dev
     wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
     assert wsb > 0
@@ -234,7 +234,8 @@ def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     a = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
     b = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
-    atomic = hk.gemm_w4a16(x, nib, sc, n, k)
+    unsplit = hk.gemm_w4a16(x, nib, sc, n, k)
+    assert torch.equal(unsplit, hk.gemm_w4a16(x, nib, sc, n, k))  # no workspace: one pass, same bits
     out = torch.empty((m, n), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
@@ -247,7 +248,7 @@ def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
         torch.cuda.synchronize()
         assert torch.equal(out, a)
     assert torch.equal(a, b)
-    assert torch.allclose(a, atomic, rtol=1e-5, atol=1e-5 * float(a.abs().max()))
+    assert torch.allclose(a, unsplit, rtol=1e-5, atol=1e-5 * float(a.abs().max()))
     wref = _round(orc.q4_to_f32(data, n, k, None), "f16").astype(np.float64)
     ref = xh.astype(np.float64) @ wref.T
     assert rel_err_floor(a.cpu().numpy(), ref) <= 2e-3
