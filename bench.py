@@ -12,9 +12,10 @@ N(0,1) with 0.5% of channels at +-20 sigma.
 One step = one pass over the suite in both precisions (W4A8: 5 GEMV launches,
 Q/K/V and gate/up each as one grouped launch, the K = 4096 ones quantizing their
 fp16 input in-kernel and down after one separate quantization launch; W4A16: 5 GEMV
-launches), captured once per weight copy as a HIP
-graph; consecutive steps use different weight copies (>= 1 GB in rotation), so the
-256 MB MALL cannot serve the weights and every byte comes from HBM.
+launches), captured as HIP graphs of four consecutive steps (plus one-step graphs for a
+remainder, so exactly K steps run); consecutive steps use different weight copies
+(>= 1 GB in rotation), so the 256 MB MALL cannot serve the weights and every byte comes
+from HBM.
 
 value = algorithmic bytes of one step / measured step time (GB/s), with the
 algorithmic bytes of a GEMV = N*K/2 (nibbles) + N*K/32*4 (f32 scales) + activation
@@ -33,7 +34,7 @@ core this process may run on (os.sched_getaffinity, as rayon's default pool) ove
 bounded sample.
 
 Also in the line (measured beside the step, not part of `value`): every suite shape
-timed on its own (graphs of 40 back-to-back launches over 8 weight copies; GB/s and
+timed on its own (graphs of 200 back-to-back launches over 8 weight copies; GB/s and
 GEMV/s), the same table at the Llama-3.2-1B shapes, the batched
 W4A8 sweep, the 3B decode step and the prefill GEMM.
 
@@ -234,6 +235,14 @@ def capture(torch, fn):
     return g
 
 
+# Launches per graph of the per-kernel tables: a graph replay costs the host-side launch
+# and the first dispatch's wait (tens of us at a replay boundary), which 200 back-to-back
+# launches amortise to about 1% of an 8B gate launch (MI355X: k_proj 2.55 -> 2.10 us,
+# gate 7.36 -> 7.20 us, lm_head 49.3 -> 48.1 us per launch from 40 to 200 launches).
+# Steps per graph of the timed step, for the same reason (a step is 11 launches).
+STEPS_PER_GRAPH = 4
+
+
 def time_graphs(torch, graphs, reps: int) -> float:
     """Replay `graphs` round-robin `reps` times; returns ms per replay."""
     torch.cuda.synchronize()
@@ -247,7 +256,7 @@ def time_graphs(torch, graphs, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40, suite=SUITE_8B):
+def kernel_table(torch, L, weights, acts, launches_per_graph: int = 200, suite=SUITE_8B):
     """Average launch duration of every (shape, precision) GEMV, each timed on its own in
     a graph of back-to-back launches over rotating weight copies.  acts: fp16 / bf16
     activations keyed "h16" / "hb" (the hidden size) and "mid16" / "midb" (the FFN
@@ -358,7 +367,7 @@ def kernel_table(torch, L, weights, acts, launches_per_graph: int = 40, suite=SU
     return rows
 
 
-def step_head_kernels(torch, step, launches_per_graph: int = 20) -> dict:
+def step_head_kernels(torch, step, launches_per_graph: int = 200) -> dict:
     """The step's two lm_head launches, each with the step's own entry point and
     arguments (same kernel instantiation as in the timed step), timed on their own: a
     graph of back-to-back launches over the rotating lm_head copies, HIP events on the
@@ -385,7 +394,7 @@ def step_head_kernels(torch, step, launches_per_graph: int = 20) -> dict:
     return res
 
 
-def batched_sweep(torch, L, weights, launches_per_graph: int = 40):
+def batched_sweep(torch, L, weights, launches_per_graph: int = 200):
     """W4A8 at M in {1,2,4,8,16} activation rows (per-row absmax
     int8, bf16 scales) on the 8B gate (14336x4096) and down (4096x14336) shapes.
     M >= 2 runs on int8 MFMA (v_mfma_i32_16x16x32_i8, 16 activation columns per
@@ -443,7 +452,7 @@ def stream_probe(torch, L) -> float:
     return buf_gbs(2 << 30, ms)
 
 
-def same_size_read(torch, L, nbytes: int, copies: int, launches_per_graph: int = 40) -> dict:
+def same_size_read(torch, L, nbytes: int, copies: int, launches_per_graph: int = 200) -> dict:
     """The streaming-read ceiling at one byte count: the library's read probe
     (nve_hip_stream_read_mode) over `copies` rotating buffers of `nbytes` each -- the
     same rotation the GEMV table uses for that shape, so the MALL serves neither more
@@ -558,12 +567,17 @@ def attn_key_split(shape, max_seq: int) -> int:
     return 1 if max_seq <= 256 else (4 if max_seq <= 1024 else cap)
 
 
+DECODE_STEPS_PER_GRAPH = 8
+
+
 def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, prefill: int = 512,
-              max_seq: int = 1024) -> dict:
+              max_seq: int = 1024, steps_per_graph: int = DECODE_STEPS_PER_GRAPH) -> dict:
     """synthetic Llama-3.2-3B decode at batch 1, greedy.  28 layers
     (a seeded 30% = 8 W4A16, 20 W4A8; W4A8 lm_head), 512 prefilled N(0,1) bf16 KV
-    positions, one HIP graph per token (all layers + head, position device-resident),
-    `tokens` greedy tokens timed with HIP events on the replay stream.  The CPU leg runs
+    positions, HIP graphs of `steps_per_graph` consecutive tokens (all layers + head per
+    token; token and position device-resident, so each step feeds the next) and a one-token
+    graph for a remainder, `tokens` greedy tokens timed with HIP events on the replay
+    stream.  The CPU leg runs
     the reference's CPU decode path (Q4 x f32 matvec_f32, AVX2 restated in oracle/, all
     projections; f32 attention) on the same weights for `cpu_tokens` tokens.  prefill /
     max_seq: the cached positions and the cache capacity (also run at 7000 / 8192 as
@@ -575,7 +589,7 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
     tokens = min(tokens, max_seq - prefill - warm - 1)
     assert tokens >= 1
     m = DecodeModel(s, max_seq=max_seq, prefill=prefill)
-    m.capture()
+    m.capture(steps_per_graph)
     m.start(1)
     m.generate(warm)
     torch.cuda.synchronize()
@@ -600,7 +614,7 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
            # down; head: final norm, lm_head (a W4A8 one leaves the argmax candidates, a
            # W4A16 one is followed by an argmax-partials launch), argmax + next embedding
            "launches_per_token": 5 * s.layers + (3 if m.lm_head_w4a8 else 4),
-           "attn_key_split": attn_key_split(s, max_seq)}
+           "attn_key_split": attn_key_split(s, max_seq), "tokens_per_graph": steps_per_graph}
     log(f"decode 3B: {ms * 1e3:.1f} us/token, {tok_s:.1f} tok/s, {rec['GBs']} GB/s")
     if not no_cpu:
         import numpy as np
@@ -694,6 +708,21 @@ def decode_traffic_probe(torch) -> None:
         m.step()
     torch.cuda.synchronize()
     log(f"decode traffic probe: 6 steps, algorithmic bytes per step {m.step_bytes()}")
+
+
+def prefill_probe(torch, hk):
+    """Eager launches for rocprofv3 --pmc of the fused prefill GEMM at large M (counter
+    collection over HIP-graph replays is not used): the 8B gate shape 14336x4096, fp16
+    x, fp16 output (one pass over K, no split), M = 512 then M = 2048, 5 launches each."""
+    g = torch.Generator(device="cuda").manual_seed(17)
+    n, k = 14336, 4096
+    nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
+    for m in (512, 2048):
+        x = torch.randn((m, k), generator=g, device="cuda").half()
+        for _ in range(5):
+            hk.gemm_w4a16(x, nib, sc, n, k, out_dtype=torch.float16)
+        torch.cuda.synchronize()
+    print(json.dumps({"probe": "prefill", "shape": f"{n}x{k}", "M": [512, 2048], "launches_each": 5}), flush=True)
 
 
 def batched_probe(torch, L, hk):
@@ -797,6 +826,8 @@ def main():
     ap.add_argument("--decode-prefill", type=int, default=512,
                     help="cached positions before the timed tokens (--decode-only)")
     ap.add_argument("--decode-max-seq", type=int, default=1024, help="KV cache slots (--decode-only)")
+    ap.add_argument("--decode-steps-per-graph", type=int, default=DECODE_STEPS_PER_GRAPH,
+                    help="tokens per replayed HIP graph in the decode measurement")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the 3B decode measurement (for profiling; no bench line)")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -806,6 +837,8 @@ def main():
     ap.add_argument("--suite-probe", action="store_true",
                     help="only the per-shape 8B table and the batched sweep, for rocprofv3 --kernel-trace "
                          "per-shape kernel durations (no bench line)")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="eager fused prefill GEMM launches at M = 512 / 2048 for rocprofv3 --pmc (no bench line)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the W4A16 prefill GEMM rows (for profiling; no bench line)")
     ap.add_argument("--decode-traffic-probe", action="store_true",
@@ -836,12 +869,16 @@ def main():
     if args.suite_probe:
         suite_probe(torch, L, hk)
         return
+    if args.prefill_probe:
+        prefill_probe(torch, hk)
+        return
     if args.prefill_only:
         print(json.dumps({"prefill_w4a16_gemm": prefill_gemm(torch, hk)}))
         return
     if args.decode_only:
         print(json.dumps({"decode_3b": decode_3b(torch, args.decode_tokens, 16, args.cpu_decode_tokens, True,
-                                                 prefill=args.decode_prefill, max_seq=args.decode_max_seq)}))
+                                                 prefill=args.decode_prefill, max_seq=args.decode_max_seq,
+                                                 steps_per_graph=args.decode_steps_per_graph)}))
         return
 
     # weight copies: layer set 136 MB -> 8 copies (1.09 GB); lm_head 328 MB -> 4 copies
@@ -858,7 +895,30 @@ def main():
     n_graphs = max(copies_layer, copies_head)
     step.run(0)
     torch.cuda.synchronize()
+    # one-step graphs (per weight copy) and STEPS_PER_GRAPH-step graphs over consecutive
+    # copies; K timed steps = K // STEPS_PER_GRAPH multi-step replays + K % STEPS_PER_GRAPH
+    # one-step replays, every step on the next weight copy
     graphs = [capture(torch, lambda ci=ci: step.run(ci)) for ci in range(n_graphs)]
+
+    def run_steps(ci0):
+        for j in range(STEPS_PER_GRAPH):
+            step.run(ci0 + j)
+    multi = [capture(torch, lambda ci=ci: run_steps(ci)) for ci in range(0, n_graphs, STEPS_PER_GRAPH)]
+
+    def time_steps(k: int) -> float:
+        """ms per step over exactly k steps (HIP events on the replay stream)."""
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        q, r = divmod(k, STEPS_PER_GRAPH)
+        for i in range(q):
+            multi[i % len(multi)].replay()
+        for j in range(r):
+            graphs[(q * STEPS_PER_GRAPH + j) % n_graphs].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / k
     # The per-shape table runs before the step is timed (same weight copies, ~10 s of
     # GPU work, no host-only gap before the step's warmup): right after set-up the step
     # runs up to 15% slower for its first few hundred replays (194, 181, 176 us for the
@@ -867,11 +927,11 @@ def main():
     # and every launch runs slower right after set-up (the first lm_head graph a process
     # times, about 10 us above the steady 49-50 us), so the table starts after 300 step
     # replays (about 50 ms)
-    time_graphs(torch, graphs, 300)
+    time_steps(300)
     log("per-kernel table:")
     table = kernel_table(torch, L, weights, acts)
-    time_graphs(torch, graphs, max(args.warmup, 1))
-    ms = time_graphs(torch, graphs, args.steps)
+    time_steps(max(args.warmup, 1))
+    ms = time_steps(args.steps)
     sb = step.step_bytes()
     value = sb / (ms * 1e-3) / 1e9
     log(f"step: {ms * 1e3:.1f} us, {sb / 1e6:.1f} MB algorithmic, {value:.1f} GB/s")
@@ -896,7 +956,7 @@ def main():
 
     layer_names = [n for n, _, _ in SUITE_8B if n != "lm_head"]
     rot_gb = round(sum(weight_bytes(n, k) * len(weights[nm]) for nm, n, k in SUITE_8B) / 1e9, 2)
-    del weights, step, graphs
+    del weights, step, graphs, multi
     torch.cuda.empty_cache()
     # the Llama-3.2-1B layer shapes, same method (16 weight copies)
     log("per-kernel table, Llama-3.2-1B shapes:")
@@ -962,7 +1022,8 @@ def main():
                         "(in-kernel for K=4096, one launch for the down input)",
             "weights_in_rotation_GB": rot_gb,
             "step_bytes": sb,
-            "graph": "one HIP graph per weight copy, replayed round-robin",
+            "graph": f"HIP graphs of {STEPS_PER_GRAPH} steps (and of 1 step for a remainder), each step on the next "
+                     "weight copy, replayed round-robin",
         },
         "roofline": roof(order[0]),
         "roofline_other": roof(order[1]),

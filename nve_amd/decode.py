@@ -292,8 +292,14 @@ class DecodeModel:
               lib().nve_hip_decode_head(C.byref(self.cfg), C.byref(self._head), self.lm_head_w4a8,
                                         torch.cuda.current_stream().cuda_stream))
 
-    def capture(self) -> None:
-        """Capture one step as a HIP graph (position and token stay device-side)."""
+    def capture(self, steps_per_graph: int = 1) -> None:
+        """Capture one step as a HIP graph (position and token stay device-side), and,
+        with steps_per_graph > 1, also that many consecutive steps as one graph: every
+        step reads the token and position the previous one left on the device, so a
+        replay of the longer graph is that many greedy tokens, with one graph launch
+        instead of one per token."""
+        if steps_per_graph < 1:
+            raise ValueError("steps_per_graph must be >= 1")
         pos0, len0 = self.pos.clone(), self.length
         hid0, tok0 = self.hidden.clone(), self.token.clone()
         self._enqueue()  # warm (kernel attributes, lazy init) before capture
@@ -301,6 +307,12 @@ class DecodeModel:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self._enqueue()
+        gm = None
+        if steps_per_graph > 1:
+            gm = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gm):
+                for _ in range(steps_per_graph):
+                    self._enqueue()
         torch.cuda.synchronize()
         # the warm-up step advanced the state (capture executes nothing): restore it; the
         # KV slot it wrote is rewritten by the next step
@@ -309,17 +321,24 @@ class DecodeModel:
         self.token.copy_(tok0)
         self.length = len0
         self.graph = g
+        self.graph_multi = gm
+        self.steps_per_graph = steps_per_graph
 
     def generate(self, n: int, use_graph: bool = True) -> None:
-        """n greedy tokens; the graph path replays the captured step."""
+        """n greedy tokens; the graph path replays the captured steps (the multi-step
+        graph while at least steps_per_graph tokens remain, then the one-step graph)."""
         if use_graph and self.graph is None:
             raise RuntimeError("capture() before generate(use_graph=True)")
         self._advance(n)
-        for _ in range(n):
-            if use_graph:
-                self.graph.replay()
-            else:
+        if not use_graph:
+            for _ in range(n):
                 self._enqueue()
+            return
+        q, r = (divmod(n, self.steps_per_graph) if getattr(self, "graph_multi", None) is not None else (0, n))
+        for _ in range(q):
+            self.graph_multi.replay()
+        for _ in range(r):
+            self.graph.replay()
 
     def step_bytes(self) -> int:
         """Algorithmic HBM bytes of one step: weights + scales of every GEMV, the KV

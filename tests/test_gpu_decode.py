@@ -145,6 +145,32 @@ def test_decode_graph_replay_matches_eager(torch_dev):
     assert int(m.pos.item()) == 40 + n
 
 
+def test_decode_multi_step_graph_matches_eager(torch_dev):
+    """Graphs of several consecutive tokens (each step reads the token and position the
+    previous one left on the device): 11 tokens as two 4-token replays and three 1-token
+    replays give the eager tokens, logits, hidden state and position bit for bit."""
+    torch = torch_dev
+    m = _model(torch, 4, 2, 64, layers=2, max_seq=96, prefill=40)
+    n = 11
+    m.start(5)
+    toks = []
+    for _ in range(n):
+        m.step()
+        toks.append(int(m.token.item()))
+    torch.cuda.synchronize()
+    logits, hidden = m.logits.cpu().clone(), m.hidden.cpu().clone()
+    m.start(5)
+    m.capture(steps_per_graph=4)
+    m.generate(4)
+    torch.cuda.synchronize()
+    assert int(m.token.item()) == toks[3] and int(m.pos.item()) == 44
+    m.generate(n - 4)
+    torch.cuda.synchronize()
+    assert int(m.token.item()) == toks[-1]
+    assert int(m.pos.item()) == 40 + n and m.length == 40 + n
+    assert torch.equal(m.logits.cpu(), logits) and torch.equal(m.hidden.cpu(), hidden)
+
+
 @pytest.mark.parametrize("split", ["2", "4", "8"])
 def test_decode_graph_replay_split_attention(torch_dev, split, monkeypatch):
     """Key-split attention (partials merged in the o_proj staging) under HIP graph
