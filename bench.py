@@ -990,7 +990,7 @@ def main():
         m = re.search(r"```json\n(.*?)\n```", tf.read_text(), re.S)
         if m:
             traffic = json.loads(m.group(1)).get("hbm_bytes_per_launch", {})
-    kernels = {"w4a8_x": "w4a8_gemv_kernel<F32, R=2, NJ=2, SRC_F16> (nve_hip_matvec_w4a8_x, lm_head 128256x4096, "
+    kernels = {"w4a8_x": "w4a8_gemv_kernel<F32, R=4, NJ=2, SRC_F16> (nve_hip_matvec_w4a8_x, lm_head 128256x4096, "
                          "fp16 input quantized in-kernel, fp32 logits)",
                "w4a16": "w4a16_gemv_kernel<bf16 x, F32 out> (nve_hip_matvec_w4a16, lm_head 128256x4096, fp32 logits)"}
     order = sorted(heads, key=lambda kk: -heads[kk]["us"])
