@@ -30,8 +30,10 @@ static constexpr int kNumCU = 256;  // MI355X
 // AUTO picks per precision from measurements on MI355X (8B layer shapes, weights
 // streamed from HBM): the W4A8 kernel is light on VALU and its one-shot form stays
 // closest to the streaming floor at every shape; the W4A16 kernel (about twice the
-// VALU work per block) gains 7-13% at the gate/up/down shapes from the persistent
-// form with one workgroup per CU, and loses at lm_head size.
+// VALU work per block) gains from the persistent form with one workgroup per CU where
+// the one-shot form's K-long LDS staging limits its workgroups per CU (K > 8192: 8B
+// down 9.0 against 10.0 us), and loses at lm_head size and, with a balanced one-shot
+// grid, at the K = 4096 shapes (8B gate 8.1 one-shot against 8.4 us).
 bool use_persistent(const W4Segs& s0, int K, bool w4a16) {
   if (g_policy == NVE_GEMV_ONESHOT || K / 32 > 64 * 8) return false;
   W4Segs s = s0;
@@ -39,7 +41,7 @@ bool use_persistent(const W4Segs& s0, int K, bool w4a16) {
     const W4Tiling t = choose_persistent_tiling(K, g_depth);
     return plan_persistent(s, t.R, 4 * kNumCU * g_occ) > 0;
   }
-  if (!w4a16) return false;
+  if (!w4a16 || K <= 8192) return false;
   long rows = 0;
   for (int i = 0; i < s.nseg; ++i) rows += s.n[i];
   const W4Tiling t = choose_persistent_tiling(K, 4);

@@ -28,9 +28,20 @@ struct W4Tiling {
   bool multi;  // K needs more than one pass of NJ chunks
 };
 
+// Excess of the busiest CU over the mean when `wgs` one-shot workgroups are dealt to
+// the 256 CUs (1.0 = every CU gets the same number).
+inline double w4_grid_imbalance(long wgs) {
+  const long rounds = (wgs + 255) / 256;
+  return (double)(rounds * 256) / (double)wgs;
+}
+
 // Rows per wave are chosen so a lane keeps about 8 blocks (160 B) of weights in
 // flight, then halved while the launch would have fewer than 512 workgroups (two per
-// CU of the 256-CU MI355X).
+// CU of the 256-CU MI355X), and halved again while that evens out the workgroups per
+// CU: all of a one-shot grid is resident at once, and a CU holding one workgroup more
+// than the others finishes a workgroup's latency later (8B gate, 14336 rows: 896
+// workgroups = 3.5 per CU at 4 rows per wave, 7.23 us W4A8 / 8.72 us W4A16; 1792 = 7
+// per CU at 2 rows, 7.05 / 8.11 us).
 inline W4Tiling choose_w4_tiling(const W4Segs& s, int K) {
   const int nb = K / 32;
   int nj = (nb + 63) / 64;
@@ -39,7 +50,14 @@ inline W4Tiling choose_w4_tiling(const W4Segs& s, int K) {
   int r = nj == 1 ? 8 : (nj == 2 ? 4 : (nj <= 4 ? 2 : 1));
   long ntot = 0;
   for (int i = 0; i < s.nseg; ++i) ntot += s.n[i];
+  auto wgs = [&](int rr) {
+    long w = 0;
+    for (int i = 0; i < s.nseg; ++i) w += (s.n[i] + 4L * rr - 1) / (4L * rr);
+    return w;
+  };
   while (r > 1 && (ntot + 4L * r - 1) / (4L * r) < 512) r /= 2;
+  while (r > 1 && w4_grid_imbalance(wgs(r)) > 1.05 && w4_grid_imbalance(wgs(r / 2)) < w4_grid_imbalance(wgs(r)))
+    r /= 2;
   return W4Tiling{r, nj, multi};
 }
 
