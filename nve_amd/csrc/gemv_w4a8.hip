@@ -50,6 +50,13 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   static_assert(PAIR != PAIR_ARGMAX || OUT_DT == NVE_DT_F32, "greedy candidates over f32 logits");
   constexpr int RH = PAIRED ? R / 2 : R;  // output rows (pairs) per wave
   constexpr int SPT = (NJ + 1) / 2;  // staging passes: 2*nb <= 128*NJ chunks of 16 B
+  // DIRECT: a pre-quantized vector (no producer) with at most two 64-block chunks per
+  // lane skips the LDS: each lane loads the int8 activations and scales of exactly the
+  // blocks it multiplies (the same blocks for all R rows), ahead of its weight loads,
+  // so no LDS write, barrier or LDS read sits between the loads and the arithmetic
+  // (8B lm_head 49.7 -> 49.1 us, q 3.55 -> 3.46; at four chunks, 1B down, it lost 0.3 us
+  // to the per-lane block sums).
+  constexpr bool DIRECT = SRC == SRC_PLAIN && !MULTI && NJ <= 2;
   extern __shared__ int4 lds[];
   const int nb = K >> 5;
   const int nchunk = 2 * nb;
@@ -74,8 +81,19 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   if constexpr (SRC != SRC_PLAIN) {
 #pragma unroll
     for (int s = 0; s < SPT; ++s) prod_issue<SRC, 16>(pc[s], pa, (int)threadIdx.x + 256 * s, nchunk);
-  } else if (!MULTI) {
+  } else if (!MULTI && !DIRECT) {
     w4a8_stage_issue<SPT>(st, xq, xs, nchunk, pa.row_scale != nullptr);
+  }
+  int4 xlo[DIRECT ? NJ : 1], xhi[DIRECT ? NJ : 1];
+  float xsr[DIRECT ? NJ : 1];
+  if constexpr (DIRECT) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int bb = min(lane + 64 * j, nb - 1);
+      xlo[j] = ((const int4*)xq)[2 * bb];
+      xhi[j] = ((const int4*)xq)[2 * bb + 1];
+      xsr[j] = pa.row_scale != nullptr ? 1.0f : xs[bb];
+    }
   }
   // Residual add (F32_ACCUM): the output rows' current values are fetched here, with
   // the staging loads, instead of by a dependent load in the epilogue.  The residual
@@ -166,6 +184,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       w4a8_stage_put(q, scale, i, i < nchunk, nb, s_lo, s_hi, s_bs);
     }
     if (kLateWeights && SRC != SRC_NORM) issue_pinned();
+  } else if (DIRECT) {
   } else if (!MULTI) {
     w4a8_stage_write<SPT>(st, s_lo, s_hi, s_bs, nchunk);
   } else {
@@ -173,7 +192,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   }
   // the weight arithmetic stays below the staging barrier
   __builtin_amdgcn_sched_barrier(0);
-  lds_barrier();
+  if constexpr (!DIRECT) lds_barrier();
 
   float acc[R];
 #pragma unroll
@@ -184,14 +203,26 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
     for (int j = 0; j < NJ; ++j) {
       const int b = jb + lane + 64 * j;
       const int bb = min(b, nb - 1);
-      const int4 lo = s_lo[bb];
-      const int4 hi = s_hi[bb];
-      const int2 bs = s_bs[bb];
+      int4 lo, hi;
+      int sumq;
+      float xsb;
+      if constexpr (DIRECT) {
+        lo = xlo[j];
+        hi = xhi[j];
+        sumq = sum_i8x16(lo) + sum_i8x16(hi);
+        xsb = xsr[j];
+      } else {
+        lo = s_lo[bb];
+        hi = s_hi[bb];
+        const int2 bs = s_bs[bb];
+        sumq = bs.x;
+        xsb = __builtin_bit_cast(float, bs.y);
+      }
       // Lanes past the end of the row contribute nothing.
-      const float xsf = b < nb ? __builtin_bit_cast(float, bs.y) : 0.0f;
+      const float xsf = b < nb ? xsb : 0.0f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int a = w4a8_block_dot(wv[r][j], lo, hi, bs.x);
+        const int a = w4a8_block_dot(wv[r][j], lo, hi, sumq);
         acc[r] = fmaf(wsc[r][j] * xsf, (float)a, acc[r]);
       }
     }
@@ -279,7 +310,8 @@ template <int OUT_DT, int R, int NJ, bool MULTI, int SRC, int PAIR>
 static hipError_t launch_w4a8_t(const int8_t* xq, const float* xs, const W4Segs& segs, int K,
                                 int grid, const nve::ProdArgs& pa, hipStream_t stream,
                                 const nve::EpiArgs& ra = nve::EpiArgs{}) {
-  const size_t lds = nve::w4a8_lds_bytes(K) + (SRC == nve::SRC_NORM ? 64 : 0);
+  constexpr bool direct = SRC == nve::SRC_PLAIN && !MULTI && NJ <= 2;  // no LDS staging (see the kernel)
+  const size_t lds = direct ? 0 : nve::w4a8_lds_bytes(K) + (SRC == nve::SRC_NORM ? 64 : 0);
   auto kern = nve::w4a8_gemv_kernel<OUT_DT, R, NJ, MULTI, SRC, PAIR>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
