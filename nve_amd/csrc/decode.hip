@@ -71,7 +71,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 // softmax(q k^T / sqrt(D)) v over the cache, and the conversion of the output to the
 // o_proj input (OUT 1: fp16, OUT 2: int8 + group-32 scales).
 //
-// One workgroup of 16 waves per query head; no cross-workgroup communication.  Keys
+// One workgroup of 8 waves per query head; no cross-workgroup communication.  Keys
 // are spread over the waves in tiles: a key's row of D bf16 (D/8 16-byte pieces)
 // sits in LPK = D/8 consecutive lanes, one piece per lane, so the q.k dot product is
 // a butterfly over those lanes and the value sum accumulates each lane's 8 columns.
@@ -79,18 +79,20 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 // softmax weight is one exp2 of a score difference.  Every wave keeps its own online
 // softmax (running max m, sum l, accumulator rescaled by 2^(m_old - m_new) when the
 // maximum grows) over its keys, with the next two tiles' K/V loads in flight while
-// the current tile is computed; the 16 wave states are merged once in LDS at the
+// the current tile is computed; the 8 wave states are merged once in LDS at the
 // end:  out = sum_w 2^(m_w - M) acc_w / sum_w 2^(m_w - M) l_w.
 // The new token's key is rotated and rounded to bf16 like every cached entry; the
 // workgroup of the kv head's first query head writes it and the value to the cache,
 // the others use their own identical copy for that row.
-// One key slot per lane per tile (64-key tiles at D = 128): against two slots (128-key
-// tiles) the 3B decode runs 1081 against 1064 tok/s at 512 cached keys and 826 against
-// 820 at 7000 -- a workgroup streams its K/V through one CU, and the smaller tile
-// shortens that stream's first wait and its tail.
+// One key slot per lane per tile (32-key tiles at D = 128): against two slots the 3B
+// decode ran 1081 against 1064 tok/s at 512 cached keys and 826 against 820 at 7000
+// (with 16 waves) -- a workgroup streams its K/V through one CU, and the smaller tile
+// shortens that stream's first wait and its tail.  Eight waves against sixteen: the
+// merge at the end combines half the wave states, 1177 against 1173.5 tok/s at 512 keys
+// (four key splits), 1168 against 1153 with eight splits, 888.6 against 881.6 at 7000.
 template <int D>
 struct AttnTile {
-  static constexpr int NW = 16;         // waves per workgroup
+  static constexpr int NW = 8;          // waves per workgroup
   static constexpr int P = 1;           // key slots per lane per tile
   static constexpr int LPK = D / 8;     // lanes per key
   static constexpr int KPW = 64 / LPK;  // keys per wave per slot
@@ -165,7 +167,7 @@ __device__ __forceinline__ void attn_compute(const AttnTile<D>& b, int t, int le
   }
 }
 
-// Merge of the 16 wave states of an attention workgroup and its output: the normalised
+// Merge of the wave states of an attention workgroup and its output: the normalised
 // head output converted to the o_proj input (OUT 1: fp16, 2: int8 + group scales), or
 // (OUT 3) the split's partial record (m, l, 0, 0, acc[D]).
 template <int D, int OUT, int SPLIT>
@@ -189,10 +191,10 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
   lds_barrier();
   if constexpr (OUT == 3) {
     // split partial record (m, l, 0, 0, acc[D]): the first D / 32 waves merge, lane l of
-    // wave w owning column 32 w + l % 32 and the waves' halves l / 32 (8 of the 16 wave
+    // wave w owning column 32 w + l % 32 and the waves' halves l / 32 (half of the wave
     // states each); the two halves meet through one xor-32 lane exchange.  Every lane
     // forms M and the weights 2^(m_w - M) itself from the broadcast maxima.
-    static_assert(D % 32 == 0 && T::NW % 2 == 0, "merge layout");
+    static_assert(D % 32 == 0 && T::NW % 2 == 0 && D / 32 <= T::NW, "merge layout");
     if (wave < D / 32) {
       const int lane = tid & 63, c = 32 * wave + (lane & 31), h = lane >> 5;
       float mw[T::NW];
@@ -222,9 +224,9 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
     }
     return;
   }
-  // one barrier: every output lane reads the 16 wave maxima and sums, forms the wave
+  // one barrier: every output lane reads the wave maxima and sums, forms the wave
   // weights 2^(m_w - M) itself (independent exp2, no second LDS round trip) and sums the
-  // 16 wave accumulators of its 4 columns
+  // wave accumulators of its 4 columns
   if (tid < D / 4) {
     float mw[T::NW], lw[T::NW];
 #pragma unroll
@@ -271,7 +273,7 @@ __device__ __forceinline__ void attn_finish(float m_run, float l_run, float (&ac
 // cache holds every row up to pos, and only the first tile's loads are issued before
 // the position is known (the others only if the split has them).
 template <int D, int OUT, int SPLIT = 1, bool PRE = false>
-__global__ __launch_bounds__(1024) void attn_decode_kernel(
+__global__ __launch_bounds__(64 * AttnTile<D>::NW) void attn_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ d_pos,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int num_heads, int num_kv_heads,
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   }
   lds_barrier();
   if (hq % G == 0 && sp == 0)
-    for (int i = tid; i < D; i += 1024) {
+    for (int i = tid; i < D; i += 64 * T::NW) {
       kc[cache_base + (size_t)pos * D + i] = s_knew[i];
       vc[cache_base + (size_t)pos * D + i] = s_vnew[i];
     }
@@ -721,7 +723,7 @@ static hipError_t launch_attention(const nve_decode_config& c, const nve_decode_
   // (kv head, split) pairs a multiple of 8: each XCD gets whole groups of query heads
   const int xcd_map = (c.num_kv_heads * split) % 8 == 0 && c.num_heads / c.num_kv_heads > 1;
 #define NVE_ATTN_P(D, OUT, S, P)                                                                             \
-  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S, P>), dim3(c.num_heads * S), dim3(1024), 0, s, ws.q, ws.k, \
+  hipLaunchKernelGGL((nve::attn_decode_kernel<D, OUT, S, P>), dim3(c.num_heads * S), dim3(64 * nve::AttnTile<D>::NW), 0, s, ws.q, ws.k, \
                      ws.v, io.k_cache, io.v_cache, io.pos, io.rope_cos, io.rope_sin, c.num_heads,                \
                      c.num_kv_heads, c.max_seq, qscale, ws.act16, ws.xq, ws.xs, ws.part, xcd_map)
 #define NVE_ATTN(D, OUT, S)          \
