@@ -1,4 +1,4 @@
-// Host-only check of the persistent GEMV grid plan (nve_amd/csrc/w4_launch.h): for
+// Host-only check of the GEMV grid plans (nve_amd/csrc/w4_launch.h).  Persistent: for
 // every wave of the grid, replays the kernel's tile walk (w4_persistent.h) and checks
 // that every pointer it would load from belongs to a real matrix, that no wave has
 // more tiles than its LDS result slots, and that every row tile is computed exactly
@@ -68,9 +68,63 @@ static void check(const int* ns, int nseg, int K, int occ, int depth) {
       CHECK(seen[i][j] == 1, "K=%d seg %d tile %zu computed %d times", K, i, j, seen[i][j]);
 }
 
+// One-shot tiling (choose_w4_tiling): the (R, NJ) it returns is a compiled case, the
+// grid covers every row, the rows-per-wave reduction never leaves the grid less
+// balanced than the rule it replaced, and the 8B gate gets the balanced 1792-workgroup
+// grid.
+static bool compiled_case(const W4Tiling& t) {
+#define NVE_CASE(RR, JJ, MM) if (t.R == RR && t.NJ == JJ && t.multi == MM) return true;
+  NVE_W4_TILING_CASES(NVE_CASE)
+#undef NVE_CASE
+  return false;
+}
+
+static void check_oneshot(const int* ns, int nseg, int K) {
+  W4Segs s{};
+  s.nseg = nseg;
+  long rows = 0;
+  for (int i = 0; i < nseg; ++i) {
+    s.n[i] = ns[i];
+    rows += ns[i];
+  }
+  const W4Tiling t = choose_w4_tiling(s, K);
+  CHECK(compiled_case(t), "K=%d rows=%ld: tiling R=%d NJ=%d not compiled", K, rows, t.R, t.NJ);
+  finalize_segments(s, t.R);
+  for (int i = 0; i < nseg; ++i) {
+    const int wgs = (i + 1 < nseg ? s.wg_begin[i + 1] : s.wg_total) - s.wg_begin[i];
+    CHECK((long)wgs * 4 * t.R >= ns[i], "K=%d seg %d: %d workgroups of %d rows miss rows of %d", K, i, wgs,
+          4 * t.R, ns[i]);
+  }
+  // against doubling R (the rows per wave the balance step may have halved)
+  if (t.R < 8) {
+    long w2 = 0;
+    for (int i = 0; i < nseg; ++i) w2 += (ns[i] + 8L * t.R - 1) / (8L * t.R);
+    const double mine = w4_grid_imbalance(s.wg_total), doubled = w4_grid_imbalance(w2);
+    CHECK(mine <= 1.05 || mine <= doubled || w2 < 512, "K=%d rows=%ld: imbalance %.3f worse than %.3f", K, rows,
+          mine, doubled);
+  }
+}
+
 int main() {
+  {
+    const int gate = 14336;
+    W4Segs s{};
+    s.nseg = 1;
+    s.n[0] = gate;
+    const W4Tiling t = choose_w4_tiling(s, 4096);
+    finalize_segments(s, t.R);
+    CHECK(t.R == 2 && s.wg_total == 1792, "8B gate: R=%d, %d workgroups", t.R, s.wg_total);
+  }
   const int Ks[] = {32, 64, 96, 2048, 3072, 4096, 8192, 14336, 16384};
   const int Ns[] = {1, 2, 3, 5, 37, 512, 1000, 1024, 3072, 4096, 8192, 14336, 128256, 151936};
+  const int Kos[] = {32, 64, 96, 2048, 3072, 4096, 8192, 14336, 16384, 16416, 32768};
+  for (int K : Kos) {
+    for (int n : Ns) check_oneshot(&n, 1, K);
+    const int qkv[3] = {3072, 1024, 1024}, odd[3] = {5, 4000, 37}, gu[2] = {14336, 14336};
+    check_oneshot(qkv, 3, K);
+    check_oneshot(odd, 3, K);
+    check_oneshot(gu, 2, K);
+  }
   for (int K : Ks)
     for (int depth = 4; depth <= 8; depth += 4)
       for (int occ = 1; occ <= 8; occ *= 2) {
