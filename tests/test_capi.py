@@ -120,10 +120,50 @@ def test_decode_argument_errors(L):
     assert call(cfg, weights(o=W4Weight(P16 + 4, P16, H, hq * D))) == -3
     assert call(cfg, iox=DecodeIO(P16, P16, P16, None, P16, P16, P16)) == -1  # pos
     assert call(cfg, iox=DecodeIO(P16, P16, P16, P16, P16, P16, P16 + 16)) == -3  # workspace alignment
+    # the stage entry point: same layer checks, plus its stage code and in / out
+    st = L.nve_hip_decode_stage
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(io), 1, 4, P16, P16, None) == -4      # stage code
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(io), 1, -1, P16, P16, None) == -4
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(io), 1, 0, None, None, None) == -1    # QKV needs out
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(io), 1, 1, None, None, None) == -1    # merge needs in
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(io), 1, 2, None, P16 + 8, None) == -3  # out alignment
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(io), 1, 3, P16 + 4, None, None) == -3  # in alignment
+    assert st(C.byref(DecodeConfig(H, hq, hkv, 96, F, 64, 512, 1e-5)), C.byref(weights()), C.byref(io), 1, 0,
+              None, P16, None) == -2
+    iow = DecodeIO(P16, P16, P16, P16, P16, P16, None)
+    assert st(C.byref(cfg), C.byref(weights()), C.byref(iow), 1, 0, None, P16, None) == -1    # workspace
     bad = DecodeHead(P16, P16, w(512, H + 32), P16, P16, P16, P16, P16)
     assert L.nve_hip_decode_head(C.byref(cfg), C.byref(bad), 1, None) == -2
     assert L.nve_hip_embed(None, P16, P16, H, None) == -1
     assert L.nve_hip_decode_workspace_bytes(C.byref(cfg)) % 256 == 0
+
+
+def test_attention_split_rule(L, monkeypatch):
+    """Key splits of the decode attention (host rule): 1 up to 256 cache slots, 4 up to
+    1024, 8 above where num_heads * head_dim <= 4096 (else 4); NVE_ATTN_SPLIT overrides
+    within that maximum."""
+    from nve_amd._lib import DecodeConfig
+    monkeypatch.delenv("NVE_ATTN_SPLIT", raising=False)
+
+    def splits(seq, heads=24, d=128):
+        return L.nve_hip_decode_attn_splits(C.byref(DecodeConfig(3072, heads, 8, d, 8192, seq, 0, 1e-5)))
+    assert [splits(s) for s in (1, 256, 257, 1024, 1025, 8192)] == [1, 1, 4, 4, 8, 8]
+    assert splits(8192, heads=48) == 4                  # 48 x 128 > 4096: four splits at most
+    for v, want in (("1", 1), ("2", 2), ("4", 4), ("8", 8), ("3", 4), ("16", 4)):
+        monkeypatch.setenv("NVE_ATTN_SPLIT", v)
+        assert splits(1024) == want, v                  # invalid values keep the default
+    monkeypatch.setenv("NVE_ATTN_SPLIT", "8")
+    assert splits(1024, heads=48) == 4
+    assert L.nve_hip_decode_attn_splits(C.byref(DecodeConfig(3072, 24, 8, 96, 8192, 64, 0, 1e-5))) == -2
+
+
+def test_stream_read_mode_argument_errors(L):
+    f = L.nve_hip_stream_read_mode
+    assert f(None, 64, P16, 0, None) == -1
+    assert f(P16, 24, P16, 1, None) == -2       # not a multiple of 16
+    assert f(P16, 0, P16, 2, None) == -2
+    assert f(P16, 64, P16, 3, None) == -4       # mode
+    assert f(P16 + 8, 64, P16, 0, None) == -3   # buffer alignment
 
 
 def test_dispatch_env_rules(L, orc, monkeypatch):
