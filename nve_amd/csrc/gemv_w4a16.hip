@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   uint4 wv[R][NJ];
   float wsc[R][NJ];
   const size_t row_bytes = (size_t)(K >> 1);
-  auto issue = [&](int jb) {
+  auto issue = [&](int jb, int e0 = 0, int e1 = R * NJ) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int rr = min(row0 + (PAIR != PAIR_NONE ? r % RH : r), N - 1);
@@ -120,6 +120,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
       const float* rs = ms + (size_t)row * nb;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
+        if (r * NJ + j < e0 || r * NJ + j >= e1) continue;
         const int bb = min(jb + lane + 64 * j, nb - 1);
         wv[r][j] = ld_stream(rn + bb);
         wsc[r][j] = ld_stream(rs + bb);
@@ -129,14 +130,20 @@ __global__ __launch_bounds__(256) void w4a16_gemv_kernel(const void* __restrict_
   // SRC_NORM / SRC_F32: weight loads issued once the norm statistic is known / the vector
   // is staged (see gemv_w4a8.hip)
   constexpr bool kLateWeights = SRC == SRC_NORM || SRC == SRC_F32;
-  if (!kLateWeights) issue(0);
+  // A late-issue launch still sends the first two of each lane's weight loads ((row,
+  // chunk) order; at most half of them) with its staging loads: the 3B decode step runs
+  // at 1196 against 1182 tok/s (512 cached keys; 893 against 885 at 7000); one or three
+  // early loads in the Q/K/V launch, one or four in gate/up, one or three in down
+  // measured equal or slower.
+  constexpr int kEarly = kLateWeights ? (R * NJ / 2 < 2 ? R * NJ / 2 : 2) : R * NJ;
+  if (kEarly > 0) issue(0, 0, kEarly);
   // A late issue is fenced on both sides so that the loads leave as one group at that
   // point: left to itself the scheduler spreads them through the quantization and hoists
   // the unpacking of the first ones above the LDS stores, which then wait for HBM before
   // the rest are even issued.
   auto issue_pinned = [&]() {
     __builtin_amdgcn_sched_barrier(0);
-    issue(0);
+    issue(0, kEarly);
     __builtin_amdgcn_sched_barrier(0);
   };
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)

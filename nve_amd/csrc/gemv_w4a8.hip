@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   uint4 wv[R][NJ];
   float wsc[R][NJ];
   const size_t row_bytes = (size_t)(K >> 1);
-  auto issue = [&](int jb) {
+  auto issue = [&](int jb, int e0 = 0, int e1 = R * NJ) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int rr = min(row0 + (PAIRED ? r % RH : r), N - 1);
@@ -126,6 +126,7 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
       const float* rs = ms + (size_t)row * nb;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
+        if (r * NJ + j < e0 || r * NJ + j >= e1) continue;
         const int b = jb + lane + 64 * j;
         const int bb = min(b, nb - 1);
         wv[r][j] = ld_stream(rn + bb);
@@ -144,14 +145,20 @@ __global__ __launch_bounds__(256) void w4a8_gemv_kernel(const int8_t* __restrict
   // just-written vector too.
   constexpr bool kLateWeights =
       SRC == SRC_NORM || SRC == SRC_F32 || (SRC == SRC_F16 && OUT_DT == NVE_DT_F32_ACCUM);
-  if (!kLateWeights) issue(0);
+  // A late-issue launch still sends the first two of each lane's weight loads ((row,
+  // chunk) order; at most half of them) with its staging loads: the 3B decode step runs
+  // at 1196 against 1182 tok/s (512 cached keys; 893 against 885 at 7000); one or three
+  // early loads in the Q/K/V launch, one or four in gate/up, one or three in down
+  // measured equal or slower.
+  constexpr int kEarly = kLateWeights ? (R * NJ / 2 < 2 ? R * NJ / 2 : 2) : R * NJ;
+  if (kEarly > 0) issue(0, 0, kEarly);
   // A late issue is fenced on both sides so that the loads leave as one group at that
   // point: left to itself the scheduler spreads them through the quantization and hoists
   // the unpacking of the first ones above the LDS stores, which then wait for HBM before
   // the rest are even issued.
   auto issue_pinned = [&]() {
     __builtin_amdgcn_sched_barrier(0);
-    issue(0);
+    issue(0, kEarly);
     __builtin_amdgcn_sched_barrier(0);
   };
   // RoPE rows of this wave's pairs (used by lane 63 in the epilogue)
