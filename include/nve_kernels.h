@@ -378,8 +378,9 @@ int nve_hip_decode_stage(const nve_decode_config *cfg, const nve_layer_weights *
 /* Key splits the layer's attention uses for cfg (1, 2, 4 or 8; NVE_ATTN_SPLIT in the
  * environment overrides, as for the layer). */
 int nve_hip_decode_attn_splits(const nve_decode_config *cfg);
-/* hidden = embed[*token] (bf16 -> fp32). */
-int nve_hip_embed(const uint16_t *embed, const int *token, float *hidden, int hidden_size,
+/* hidden = embed[*token] (bf16 -> fp32), embed [vocab, hidden_size].  The token is read
+ * on the device: one outside [0, vocab) is clamped into it (no out-of-table read). */
+int nve_hip_embed(const uint16_t *embed, const int *token, float *hidden, int hidden_size, int vocab,
                   void *stream);
 
 /* ---- measurement and diagnostics ------------------------------------------ */

@@ -63,7 +63,7 @@ SIGNATURES: dict[str, tuple] = {
     "nve_hip_decode_stage": (_i, [_p, _p, _p, _i, _i, _p, _p, _p]),
     "nve_hip_decode_attn_splits": (_i, [_p]),
     "nve_hip_decode_head": (_i, [_p, _p, _i, _p]),
-    "nve_hip_embed": (_i, [_p, _p, _p, _i, _p]),
+    "nve_hip_embed": (_i, [_p, _p, _p, _i, _i, _p]),
     "nve_hip_last_status": (_i, []),
     "nve_hip_status_string": (C.c_char_p, [_i]),
     "nve_hip_version": (C.c_char_p, []),

@@ -489,10 +489,11 @@ int nve_hip_decode_head(const nve_decode_config* cfg, const nve_decode_head* hd,
   return set_status(decode_head(*cfg, *hd, use_w4a8 != 0, (hipStream_t)stream));
 }
 
-int nve_hip_embed(const uint16_t* embed, const int* token, float* hidden, int hidden_size, void* stream) {
+int nve_hip_embed(const uint16_t* embed, const int* token, float* hidden, int hidden_size, int vocab,
+                  void* stream) {
   if (!embed || !token || !hidden) return set_status(NVE_ERR_NULL);
-  if (hidden_size < 1) return set_status(NVE_ERR_SHAPE);
-  return from_hip(launch_embed(embed, token, hidden, hidden_size, (hipStream_t)stream));
+  if (hidden_size < 1 || vocab < 1) return set_status(NVE_ERR_SHAPE);
+  return from_hip(launch_embed(embed, token, hidden, hidden_size, vocab, (hipStream_t)stream));
 }
 
 // ---- kernel selection ---------------------------------------------------------------

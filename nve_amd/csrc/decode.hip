@@ -587,9 +587,10 @@ __global__ __launch_bounds__(1024) void argmax_embed_kernel(const float* __restr
 }
 
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__ embed, const int* __restrict__ token,
-                                                    float* __restrict__ hidden, int H) {
+                                                    float* __restrict__ hidden, int H, int vocab) {
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < H) hidden[i] = bf16_bits_to_f32(embed[(size_t)(*token) * H + i]);
+  const int t = min(max(*token, 0), vocab - 1);  // a token outside the table is clamped into it
+  if (i < H) hidden[i] = bf16_bits_to_f32(embed[(size_t)t * H + i]);
 }
 
 }  // namespace nve
@@ -924,8 +925,8 @@ int decode_head(const nve_decode_config& c, const nve_decode_head& hd, bool w4a8
   return (int)hipGetLastError();
 }
 
-hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s) {
-  hipLaunchKernelGGL(nve::embed_kernel, dim3((H + 255) / 256), dim3(256), 0, s, embed, token, hidden, H);
+hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, int vocab, hipStream_t s) {
+  hipLaunchKernelGGL(nve::embed_kernel, dim3((H + 255) / 256), dim3(256), 0, s, embed, token, hidden, H, vocab);
   return hipGetLastError();
 }
 

@@ -219,7 +219,7 @@ hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W
                              hipStream_t stream, const nve::EpiArgs& ra);
 hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                               hipStream_t stream, const nve::EpiArgs& ra);
-hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, hipStream_t s);
+hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, int vocab, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);
 hipError_t launch_w4a8_rowscale(const int8_t* xq, const uint16_t* row_scale, const W4Segs& segs, int out_dt, int K,

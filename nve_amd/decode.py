@@ -261,7 +261,7 @@ class DecodeModel:
         self.length = self.prefill
         self.token.fill_(int(token))
         check("nve_hip_embed", lib().nve_hip_embed(self.embed.data_ptr(), self.token.data_ptr(),
-                                                    self.hidden.data_ptr(), self.shape.hidden,
+                                                    self.hidden.data_ptr(), self.shape.hidden, self.shape.vocab,
                                                     torch.cuda.current_stream().cuda_stream))
 
     def _advance(self, n: int) -> None:

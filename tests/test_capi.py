@@ -134,7 +134,8 @@ def test_decode_argument_errors(L):
     assert st(C.byref(cfg), C.byref(weights()), C.byref(iow), 1, 0, None, P16, None) == -1    # workspace
     bad = DecodeHead(P16, P16, w(512, H + 32), P16, P16, P16, P16, P16)
     assert L.nve_hip_decode_head(C.byref(cfg), C.byref(bad), 1, None) == -2
-    assert L.nve_hip_embed(None, P16, P16, H, None) == -1
+    assert L.nve_hip_embed(None, P16, P16, H, 512, None) == -1
+    assert L.nve_hip_embed(P16, P16, P16, H, 0, None) == -2
     assert L.nve_hip_decode_workspace_bytes(C.byref(cfg)) % 256 == 0
 
 

@@ -379,3 +379,19 @@ def test_head_with_caller_logits_and_more_rows_than_vocab(torch_dev, lm8):
         print(f"lm8={lm8} step {step}: token {tok} / {int(tok2.item())}", flush=True)
         assert np.array_equal(lg2[:vocab], lg) and np.array_equal(lg2[vocab:], lg[:extra])
         assert int(tok2.item()) == tok
+
+
+def test_embed_token_clamped(torch_dev):
+    """nve_hip_embed: the row of the token, bf16 -> fp32 exactly; a token outside
+    [0, vocab) (read on the device) is clamped to the first / last row."""
+    torch = torch_dev
+    from nve_amd._lib import lib
+    vocab, H = 37, 200
+    emb = torch.randn((vocab, H), device="cuda").to(torch.bfloat16)
+    hidden = torch.empty(H, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    for tok, row in ((5, 5), (vocab - 1, vocab - 1), (vocab + 9, vocab - 1), (-4, 0)):
+        t = torch.tensor([tok], dtype=torch.int32, device="cuda")
+        assert lib().nve_hip_embed(emb.data_ptr(), t.data_ptr(), hidden.data_ptr(), H, vocab, s) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(hidden, emb[row].float()), (tok, row)
