@@ -643,13 +643,14 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
 def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     """The prefill-adjacency row: W4A16 GEMM X[M, K] @ W^T at the 8B gate shape
     (14336 x 4096), fp16 activations, fp32 output, M in {1, 4, 16, 128, 512, 2048}: the
-    fused MFMA kernels of nve_hip_gemm_w4a16 (weight-streaming for M <= 16, tiled above)
+    fused MFMA kernels of nve_hip_gemm_w4a16 (weight-streaming up to M = 192, 256 x 128
+    output tiles from M = 256)
     against the reference's own method on the same GPU
     (nve_dequant_w4a16 to fp16, then a dense fp16 GEMM -- torch.matmul, i.e. the
     vendor BLAS -- as GpuWeight::matmul_x does with candle, src/gpu_layer.rs:219-237).
     Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time.
-    library_us: nve_hip_gemm_w4a16_ws with its workspace (dequant + hipBLASLt from
-    M = 512 on, the fused kernels below), fp32 output; library_f16_out_us: the same
+    library_us: nve_hip_gemm_w4a16_ws with its workspace (dequant + hipBLASLt above
+    M = 512, the fused kernels up to it), fp32 output; library_f16_out_us: the same
     with fp16 output, the output type of the reference-method timing."""
     g = torch.Generator(device="cuda").manual_seed(17)
     n, k = 14336, 4096
@@ -688,9 +689,9 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
                             "dequant_plus_blas_us": round(us_ref, 1),
                             "library_us": round(us_lib, 1),
                             "library_f16_out_us": round(us_lib16, 1),
-                            # the library's rule (gemm_blas.hip): dequant + hipBLASLt from M = 512
-                            # with a workspace; below it the workspace holds K-split partials
-                            "library_path": "dequant + hipBLASLt" if m >= 512 and wsb else "fused"})
+                            # the library's rule (gemm_blas.hip): dequant + hipBLASLt above M = 512
+                            # with a workspace; up to it the fused kernels
+                            "library_path": "dequant + hipBLASLt" if m > 512 and wsb else "fused"})
         log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us, "
             f"nve_hip_gemm_w4a16_ws {us_lib:.1f} us (fp16 out {us_lib16:.1f} us)")
         del x, wf, ws

@@ -227,7 +227,8 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * then a dense GEMM) in one kernel: each weight is rounded exactly as the dequant
  * rounds it (to x's dtype: F16 as the reference, or BF16) and the products accumulate
  * in fp32 on MFMA (M <= 320: weight-streaming kernels, where K % 128 == 0 and N <= 16384 an
- * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; larger M: LDS-tiled).  x [M, K]
+ * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; from M = 256
+ * without awq: 256 x 128 output tiles; otherwise 128 x 128 tiles).  x [M, K]
  * row-major F16/BF16 (16-byte aligned); awq [K] or NULL; out [M, N] row-major F16,
  * BF16 or F32.  K % 64 == 0.  Bit-reproducible: the same inputs give the same bits on
  * every call (no atomic accumulation; nve_hip_gemm_w4a16_ws can also split K over
@@ -239,7 +240,7 @@ int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles
 /* The same product with the reference's own two-step method where it is faster
  * (GpuWeight::matmul_x, src/gpu_layer.rs:219-237), and bit-reproducible everywhere.
  * The workspace (nve_hip_gemm_w4a16_workspace_bytes(M, N, K) bytes, 256-byte aligned)
- * holds: for M >= 512, with out F32 or x's dtype, the weights dequantized by
+ * holds: for M > 512, with out F32 or x's dtype, the weights dequantized by
  * nve_hip_dequant_w4 (bit-identical to the reference dequant), which hipBLASLt then
  * multiplies with fp32 accumulation; otherwise the fp32 partials of the fused kernel's
  * K split, added in a fixed order (0 bytes when the shape does not split).  With a NULL

@@ -2,9 +2,9 @@
 //
 // GpuWeight::matmul_x (src/gpu_layer.rs:219-237) expands the int4 weights to a dense
 // 16-bit matrix with nve_dequant_w4a16 and multiplies with the vendor GEMM.  The fused
-// kernel of gemm_w4a16.hip wins while weight traffic dominates (M <= ~128) but
-// re-dequantizes each weight slice once per 128-row tile, so from M = 512 on the
-// reference's two-step method is the faster one on this part.  nve_hip_gemm_w4a16_ws
+// kernels (gemm_w4a16.hip, gemm_w4a16_tile.hip) win up to M = 512; they re-dequantize
+// each weight slice once per activation row block, so above M = 512 the reference's
+// two-step method is the faster one on this part.  nve_hip_gemm_w4a16_ws
 // takes that path when the caller provides the workspace: the weights are dequantized
 // into it (dequant_w4_kernel, bit-identical to the reference dequant) and hipBLASLt
 // computes Y = X W^T with fp32 accumulation.  Column-major view: D (N x M, ld N) =
@@ -32,7 +32,9 @@ size_t gemm_split_parts_bytes(int M, int N, int K);
 
 namespace {
 
-constexpr int kGemmBlasMinM = 512;        // from here on dequant + GEMM is faster
+// from here on dequant + GEMM is faster (8B gate, fp16 out: 102.5 us at M = 640 against
+// 165.6 for the tile kernel; at M = 512 the tile kernel's 83.6 beats its 94.1)
+constexpr int kGemmBlasMinM = 513;
 constexpr size_t kBlasWorkspace = 32u << 20;
 constexpr int kBlasCandidates = 32;  // heuristic candidates timed on the first call per shape
 constexpr int kBlasTimedRuns = 5;    // timed runs per candidate (after one untimed run)

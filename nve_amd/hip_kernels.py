@@ -275,7 +275,7 @@ def gemm_w4a16_ws(x: torch.Tensor, nibbles: torch.Tensor, scales: torch.Tensor, 
                   workspace: torch.Tensor | None, awq: torch.Tensor | None = None,
                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """gemm_w4a16 with the reference's two-step method (dequant + vendor GEMM) where it
-    is faster (M >= 512, given `workspace` of gemm_w4a16_workspace_bytes bytes)."""
+    is faster (M > 512, given `workspace` of gemm_w4a16_workspace_bytes bytes)."""
     m = x.shape[0]
     out = torch.empty((m, n), dtype=out_dtype, device=x.device)
     ws_ptr = None if workspace is None else _dev(workspace, "workspace")

@@ -44,7 +44,8 @@ def _round(a, dt):
                                    (1, 4097, 256), (4, 14336, 4096), (9, 4096, 14336), (16, 16384, 512),
                                    (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256), (48, 14336, 4096),
                                    (100, 2000, 1024), (48, 16400, 512), (33, 200, 4160), (64, 14336, 4096), (60, 300, 512), (320, 1000, 1024), (129, 700, 512),
-                                   (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192)])
+                                   (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192),
+                                   (300, 1000, 512), (600, 520, 2048), (1100, 300, 1024)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_parity(orc, torch_dev, hk, m, n, k, xdt, with_awq):
@@ -114,6 +115,33 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
     assert np.array_equal(got.T.view(np.uint32), wref.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 130, 256), (300, 1000, 512), (257, 129, 192), (1100, 300, 1024)])
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n, k, xdt):
+    """From M = 256 without AWQ the 256 x 128-tile kernel runs (gemm_w4a16_tile.hip).
+    One-hot activation rows (row i picks column k_i) make each output one product
+    1 * w, so Y[i, :] is weight column k_i as the kernel rounded it, which must equal the
+    reference dequant bit for bit.  Ragged M and N, K % 128 == 64 (K = 192), and tile
+    grids that are not a multiple of 8 workgroups (the XCD-grouped tile order: 2 x 2,
+    2 x 8, 2 x 2 and 5 x 3 tiles); fp32 output, and fp16 output for fp16 x (exact too)."""
+    torch = torch_dev
+    print(f"tile identity m={m} n={n} k={k} x={xdt}", flush=True)
+    data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.3))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    wref = _round(orc.q4_to_f32(data, n, k, None), xdt)
+    ks = np.random.default_rng(m + k).integers(0, k, m)
+    tdt = torch.float16 if xdt == "f16" else torch.bfloat16
+    x = torch.zeros((m, k), dtype=tdt, device="cuda")
+    x[torch.arange(m, device="cuda"), torch.from_numpy(ks).cuda()] = 1
+    tn, ts = torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda()
+    y = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), np.ascontiguousarray(wref[:, ks].T).view(np.uint32))
+    if xdt == "f16":
+        y16 = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.float16)
+        assert np.array_equal(y16.cpu().numpy(), wref[:, ks].T.astype(np.float16))
+
+
 @pytest.mark.parametrize("odt,tol", [("bf16", 2.0 ** -8 + 2e-3), ("f16", 2.0 ** -11 + 2e-3)])
 @pytest.mark.parametrize("m", [33, 5])
 def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
@@ -132,11 +160,11 @@ def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
     assert rel_err_floor(y.float().cpu().numpy(), ref) <= tol
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 256, 1024), (600, 520, 2048), (1024, 384, 4096)])
+@pytest.mark.parametrize("m,n,k", [(520, 256, 1024), (600, 520, 2048), (1024, 384, 4096)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_ws_blas_path(orc, torch_dev, hk, m, n, k, xdt, with_awq):
-    """nve_hip_gemm_w4a16_ws at M >= 512 with its workspace: dequant (bit-identical
+    """nve_hip_gemm_w4a16_ws above M = 512 with its workspace: dequant (bit-identical
     weights) + hipBLASLt, the reference's own prefill method, to the same bar."""
     torch = torch_dev
     print(f"gemm_ws m={m} n={n} k={k} x={xdt} awq={with_awq}", flush=True)
@@ -166,18 +194,19 @@ def test_gemm_w4a16_ws_blas_path(orc, torch_dev, hk, m, n, k, xdt, with_awq):
 
 
 def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
-    """Below M = 512, or without a workspace, nve_hip_gemm_w4a16_ws is the fused kernel
+    """Up to M = 512, or without a workspace, nve_hip_gemm_w4a16_ws is the fused kernel
     (compared at fp16 output: with a workspace an fp32 product at small M splits K, whose
     partials then add in a different order than one pass)."""
     torch = torch_dev
-    # below M = 512 the workspace holds only K-split partials (none for M <= 16)
+    # up to M = 512 the workspace holds only K-split partials (none for M <= 16)
     assert hk.gemm_w4a16_workspace_bytes(16, 256, 1024) == 0
     assert hk.gemm_w4a16_workspace_bytes(511, 256, 1024) == 4 * 511 * 256 * 4
-    assert hk.gemm_w4a16_workspace_bytes(512, 256, 1024) > (256 * 1024 * 2)
+    assert hk.gemm_w4a16_workspace_bytes(512, 256, 1024) == 4 * 512 * 256 * 4
+    assert hk.gemm_w4a16_workspace_bytes(513, 256, 1024) > (256 * 1024 * 2)
     n, k = 256, 1024
     data = orc.q4_from_f32(weights(n, k, seed=5, std=0.05))
     nib, sc = (torch.from_numpy(a).cuda() for a in orc.extract_for_gpu(data, n, k))
-    for m in (64, 600):
+    for m in (64, 300, 512, 600):
         x = torch.randn((m, k), device="cuda").to(torch.float16)
         a = hk.gemm_w4a16(x, nib, sc, n, k, out_dtype=torch.float16).cpu()
         b = hk.gemm_w4a16_ws(x, nib, sc, n, k, None, out_dtype=torch.float16).cpu()
