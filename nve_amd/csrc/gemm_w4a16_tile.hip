@@ -6,17 +6,19 @@
 // (f32 fma(n, s, -8 s) = (n - 8) s, then RNE to the activation type) but only in registers.
 //
 // Tile: 256 x 128 outputs per workgroup of 4 waves (2 x 2), 128 x 64 per wave as 4 x 2
-// tiles of v_mfma_f32_32x32x16; K advances 64 per slice (two Q4 blocks).
-//   * Activation slices: global -> LDS transfers (buffer_load ... lds) two slices ahead
-//     into a three-slot ring; the A operands are read from LDS (ds_read_b128).
+// tiles of v_mfma_f32_32x32x16; K advances 64 per slice (two Q4 blocks), two slices per
+// barrier (the barrier and each slice's first LDS reads cost about 450 cycles of a
+// 2,700-cycle slice).
+//   * Activation slices: global -> LDS transfers (buffer_load ... lds) one iteration ahead
+//     into two slots of two slices; the A operands are read from LDS (ds_read_b128).
 //   * Weights: the raw blocks (16 B of nibbles and the f32 scale per block row) go to a
-//     five-slot LDS ring four slices ahead; each wave reads the 8-byte nibble runs of its
+//     three-slot LDS ring two iterations ahead; each wave reads the 8-byte nibble runs of its
 //     64 rows once per slice and forms its B operands in registers (v_cvt_f32_ubyte, fma,
 //     v_cvt_pk), spread between its MFMAs.  The two waves sharing a column block both
 //     dequantize it; that VALU work runs beside the matrix pipe, while an LDS copy of the
 //     dequantized weights would cost more LDS bandwidth than the MFMAs leave (measured:
 //     one ds_read_b128 per 32x32x16 MFMA already stretches it from 33 to 47 cycles).
-//   * One barrier per slice.
+//   * One barrier per two slices.
 // LDS rows of the activation ring are 128 B (8 chunks of 8 values); chunk c of row r sits
 // at chunk position c ^ ((r >> 1) & 7), so the 16 lanes of each ds_read_b128 phase
 // (rows r .. r + 15 of one chunk) cover all 64 banks.  LDS reads are inline asm with
@@ -32,12 +34,12 @@
 namespace nve {
 
 constexpr int TL_BM = 256, TL_BN = 128, TL_BK = 64;
-constexpr int TL_X = TL_BM * TL_BK * 2;  // 32 KiB: 256 rows x 64 values
-constexpr int TL_R = TL_BN * 2 * 20;     // 5 KiB: 256 blocks x (16 B nibbles, 4 B scale)
-constexpr int TL_RS = 5;                 // raw weight slots: issued TL_RS - 1 slices ahead
-constexpr int TL_R0 = 3 * TL_X;
-constexpr int TL_LDS = TL_R0 + TL_RS * TL_R;  // 121 KiB
-constexpr int TL_LOADS = 8 + 2;               // transfers per thread and slice (activations, raw)
+constexpr int TL_X = TL_BM * TL_BK * 2;  // 32 KiB: one 64-wide slice, 256 rows x 64 values
+constexpr int TL_R = TL_BN * 2 * 20;     // 5 KiB: one slice's 256 blocks x (16 B nibbles, 4 B scale)
+// An iteration (one barrier) covers two slices: two activation slots of two slices each,
+// three raw weight slots of two slices each
+constexpr int TL_R0 = 2 * 2 * TL_X;
+constexpr int TL_LDS = TL_R0 + 3 * 2 * TL_R;  // 158 KiB
 
 typedef _Float16 tl_h8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 tl_b8_t __attribute__((ext_vector_type(8)));
@@ -165,19 +167,19 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   // which keeps every iteration's transfer count equal)
   auto issue_raw = [&](int t, int rslot) {
     const int tc = min(t, T - 1);
-    char* const rb = tl_lds + TL_R0 + rslot * TL_R;
+    char* const rb = tl_lds + TL_R0 + (2 * rslot + (t & 1)) * TL_R;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(nr, (lds_void_t*)(rb + wave * 1024), 16, noff, tc * 32, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void_t*)(rb + 4096 + wave * 256), 4, soff, tc * 8, 0, 0);
   };
   // activation transfers i0 .. i1 - 1 of slice t
   auto issue_x_part = [&](int t, int xslot, int i0, int i1) {
     const int ko = min(t, T - 1) * (TL_BK * 2);
-    char* const base = tl_lds + xslot * TL_X + wave * 64 * 128;
+    char* const base = tl_lds + (2 * xslot + (t & 1)) * TL_X + wave * 64 * 128;
 #pragma unroll
     for (int i = i0; i < i1; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(base + i * 1024), 16, xoff[i], ko, 0, 0);
   };
-  auto issue_x = [&](int t, int xslot) { issue_x_part(t, xslot, 0, 8); };
+  auto issue_x = [&](int t, int xslot) { issue_x_part(t, xslot, 0, 8); };  // slice t into its half of xslot
   auto rd_a = [&](uint32_t xa, int kk, u32x4_t (&fa)[4]) {
     const uint32_t a = xa + arow + koff[kk];
     fa[0] = tl_ds_read128<0>(a);
@@ -191,13 +193,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     const uint32_t hi = (kk & 1) ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
     return tl_dequant8<BF16>(lo, hi, s, -8.0f * s);
   };
-  // the MFMAs of one slice: A fragments of step kk + 1 are read and B operands of step
-  // kk + 1 formed while step kk multiplies (each MFMA followed by VALU work); the
-  // transfers of later slices (raw weights tr, activations tx) leave beside the MFMAs too:
-  // issued back to back after the barrier, the four waves' 40 transfers held the address
-  // pipeline for about 500 cycles with no matrix work in flight
-  auto mma = [&](int xslot, int rslot, int tr, int rslot_r, int tx, int xslot_x) {
-    const uint32_t xa = lds0 + xslot * TL_X, rb = lds0 + TL_R0 + rslot * TL_R;
+  // the MFMAs of one slice (activations at LDS xa, raw weights at rb): A fragments of step
+  // kk + 1 are read and B operands of step kk + 1 formed while step kk multiplies (each
+  // MFMA followed by VALU work); iss(kk) issues transfers of later slices beside the
+  // MFMAs of step kk: issued back to back after the barrier, the four waves' transfers
+  // held the address pipeline for about 500 cycles with no matrix work in flight
+  auto mma = [&](uint32_t xa, uint32_t rb, auto&& iss) {
     tl_u2_t q[2][2];  // [j][block]
     uint32_t sbits[2][2];
     u32x4_t fa[4];
@@ -237,14 +238,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
 #pragma unroll
       for (int j = 0; j < 2; ++j) cb[j] = fb[j];
       if (kk < 3) rd_a(xa, kk + 1, fa);
-      if (kk == 0) {
-        issue_raw(tr, rslot_r);
-        issue_x_part(tx, xslot_x, 0, 2);
-      } else if (kk == 1) {
-        issue_x_part(tx, xslot_x, 2, 5);
-      } else if (kk == 2) {
-        issue_x_part(tx, xslot_x, 5, 8);
-      }
+      iss(kk);
       // one scheduling region: the 8 MFMAs of step kk with the next step's B operands
       // formed between them
       if (kk < 3) {
@@ -265,32 +259,39 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     }
   };
 
-  // Pipeline (one barrier per slice): iteration t multiplies slice t (activation slot
-  // t % 3, raw weight slot t % TL_RS) and issues the transfers of raw weights
-  // t + TL_RS - 1 (into the slot slice t - 1 left) and activations t + 2 (TL_LOADS per
-  // thread).  At the top of iteration t, this thread's transfers of activations t and raw
-  // weights t are the ones older than the last TL_LOADS; the barrier then makes every
-  // thread's transfers visible.  Prologue order raw 0 .. TL_RS - 3, x 0, raw TL_RS - 2,
-  // x 1: the top of iteration 0 needs x 0 and raw 0, older than the last TL_LOADS
-  // (raw TL_RS - 2, x 1) -- as in the steady state, where iteration t - 1 issued
-  // raw t + TL_RS - 2 and x t + 1.
-#pragma unroll
-  for (int u = 0; u < TL_RS - 2; ++u) issue_raw(u, u);
+  // Pipeline: iteration u (one barrier) multiplies slices 2u and 2u + 1 (activation slot
+  // u % 2, raw weight slot u % 3); beside the MFMAs of slice 2u it issues the activation
+  // transfers of slices 2u + 2 and 2u + 3 (16 per thread, into the slot iteration u - 1
+  // read), beside those of slice 2u + 1 the raw weight transfers of slices 2u + 4 and
+  // 2u + 5 (4 per thread, into the slot iteration u - 1 read).  At the top of iteration u
+  // this thread's activation transfers for it and raw transfers (issued an iteration
+  // earlier still) are all but the last 4 (the raw transfers of iteration u - 1); the
+  // barrier then makes every thread's transfers visible and every read of the slots about
+  // to be refilled finished.  Prologue order raw 0-1, x 0-1, raw 2-3: the same at u = 0.
+  issue_raw(0, 0);
+  issue_raw(1, 0);
   issue_x(0, 0);
-  issue_raw(TL_RS - 2, TL_RS - 2);
-  issue_x(1, 1);
+  issue_x(1, 0);
+  issue_raw(2, 1);
+  issue_raw(3, 1);
 
-  int xs = 0, rs = 0;  // slots of activations t and raw weights t
-  for (int t = 0; t < T; ++t) {
-    const int xs2 = xs == 0 ? 2 : xs - 1;          // (t + 2) % 3
-    const int rs1 = rs == 0 ? TL_RS - 1 : rs - 1;  // (t - 1) % TL_RS = (t + TL_RS - 1) % TL_RS
-    wait_vmcnt<TL_LOADS>();
+  int xs = 0, rs = 0;  // slots of iteration u's activations and raw weights
+  for (int t = 0; t < T; t += 2) {
+    const int rs2 = rs == 0 ? 2 : rs - 1;  // (u + 2) % 3 = (u - 1) % 3
+    wait_vmcnt<4>();
     lgkm_wait();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    mma(xs, rs, t + TL_RS - 1, rs1, t + 2, xs2);
-    xs = xs == 2 ? 0 : xs + 1;
-    rs = rs == TL_RS - 1 ? 0 : rs + 1;
+    const uint32_t xa = lds0 + 2 * xs * TL_X, rb = lds0 + TL_R0 + 2 * rs * TL_R;
+    mma(xa, rb, [&](int kk) {
+      issue_x_part(t + 2 + (kk >> 1), xs ^ 1, 4 * (kk & 1), 4 * (kk & 1) + 4);
+    });
+    mma(xa + TL_X, rb + TL_R, [&](int kk) {
+      if (kk == 0) issue_raw(t + 4, rs2);
+      if (kk == 1) issue_raw(t + 5, rs2);
+    });
+    xs ^= 1;
+    rs = rs == 2 ? 0 : rs + 1;
   }
   // the transfers issued past the last slice (clamped re-reads) land before the
   // workgroup's LDS is released
@@ -315,9 +316,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
 
 namespace nve_host {
 
-// The tile kernel serves K % 64 == 0 without AWQ, with 32-bit activation offsets.
+// The tile kernel serves K % 128 == 0 (two slices per iteration) without AWQ, with 32-bit
+// activation offsets.
 bool gemm_tile_fits(int M, int N, int K, bool awq) {
-  return !awq && K % 64 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30);
+  return !awq && K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30);
 }
 
 template <bool BF16, int OUT_DT>
@@ -340,7 +342,7 @@ static hipError_t launch_tile_t(const void* x, int M, const uint8_t* nib, const 
 
 hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, void* out,
                                   int out_dt, int N, int K, hipStream_t s) {
-  if (K % nve::TL_BK != 0) return hipErrorInvalidValue;
+  if (K % (2 * nve::TL_BK) != 0) return hipErrorInvalidValue;
   const bool bf = x_dt == NVE_DT_BF16;
 #define NVE_TL(B)                                                                       \
   switch (out_dt) {                                                                     \

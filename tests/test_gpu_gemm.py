@@ -115,15 +115,17 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
     assert np.array_equal(got.T.view(np.uint32), wref.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 130, 256), (300, 1000, 512), (257, 129, 192), (1100, 300, 1024)])
+@pytest.mark.parametrize("m,n,k", [(256, 130, 256), (300, 1000, 512), (257, 129, 256), (1100, 300, 1024), (300, 200, 192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n, k, xdt):
-    """From M = 256 without AWQ the 256 x 128-tile kernel runs (gemm_w4a16_tile.hip).
+    """From M = 256 without AWQ and with K % 128 == 0 the 256 x 128-tile kernel runs
+    (gemm_w4a16_tile.hip; K % 128 == 64, here K = 192, the 128 x 128-tile kernel).
     One-hot activation rows (row i picks column k_i) make each output one product
     1 * w, so Y[i, :] is weight column k_i as the kernel rounded it, which must equal the
-    reference dequant bit for bit.  Ragged M and N, K % 128 == 64 (K = 192), and tile
-    grids that are not a multiple of 8 workgroups (the XCD-grouped tile order: 2 x 2,
-    2 x 8, 2 x 2 and 5 x 3 tiles); fp32 output, and fp16 output for fp16 x (exact too)."""
+    reference dequant bit for bit.  Ragged M and N, K = 256 (one iteration of two
+    slices), and tile grids that are not a multiple of 8 workgroups (the XCD-grouped
+    tile order: 2 x 2, 2 x 8, 2 x 2 and 5 x 3 tiles); fp32 output, and fp16 output for
+    fp16 x (exact too)."""
     torch = torch_dev
     print(f"tile identity m={m} n={n} k={k} x={xdt}", flush=True)
     data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.3))
