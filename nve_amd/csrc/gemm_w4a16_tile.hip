@@ -316,10 +316,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
 
 namespace nve_host {
 
-// The tile kernel serves K % 128 == 0 (two slices per iteration) without AWQ, with 32-bit
-// activation offsets.
+// The tile kernel serves K % 128 == 0 (two slices per iteration) without AWQ, where every
+// byte offset fits its buffer resource (2^31 - 1 bytes; reads past it would return zeros):
+// activations M K, nibbles N K / 2 and scales N K / 8 bytes.
 bool gemm_tile_fits(int M, int N, int K, bool awq) {
-  return !awq && K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30);
+  return !awq && K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30) && (long)N * (K / 2) < (1L << 31);
 }
 
 template <bool BF16, int OUT_DT>
