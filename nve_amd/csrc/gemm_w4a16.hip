@@ -766,9 +766,9 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
-  // from M = 256 (no AWQ, K % 64 == 0) the 256 x 128-tile kernel of gemm_w4a16_tile.hip
-  // (8B gate, fp16 out: 83.4 us at M = 256, 83.6 at 512, 171 at 1024, against 86.3 / 102.8
-  // / 218 us for the ring launches and the 128 x 128-tile kernel below)
+  // from M = 256 (no AWQ, K % 128 == 0) the 256 x 128-tile kernel of gemm_w4a16_tile.hip
+  // (8B gate, fp16 out: 66.0 us at M = 256, 73.6 at 512, 149.8 at 1024, against 86.3 / 102.8
+  // / 218.3 us for the ring launches and the 128 x 128-tile kernel below)
   if (M >= kGemmTileMinM && gemm_tile_fits(M, N, K, awq != nullptr))
     return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, out, out_dt, N, K, s);
   // up to M = 320 (AWQ: 128) where the ring fits: ring launches of up to 64 (AWQ: 32)
