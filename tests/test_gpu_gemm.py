@@ -124,8 +124,8 @@ def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n,
     1 * w, so Y[i, :] is weight column k_i as the kernel rounded it, which must equal the
     reference dequant bit for bit.  Ragged M and N, K = 256 (one iteration of two
     slices), and tile grids that are not a multiple of 8 workgroups (the XCD-grouped
-    tile order: 2 x 2, 2 x 8, 2 x 2 and 5 x 3 tiles); fp32 output, and fp16 output for
-    fp16 x (exact too)."""
+    tile order: 2 x 2, 2 x 8, 2 x 2 and 5 x 3 tiles); fp32 output, and fp16 / bf16 output
+    for fp16 / bf16 x (exact too)."""
     torch = torch_dev
     print(f"tile identity m={m} n={n} k={k} x={xdt}", flush=True)
     data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.3))
@@ -142,10 +142,14 @@ def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n,
     if xdt == "f16":
         y16 = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.float16)
         assert np.array_equal(y16.cpu().numpy(), wref[:, ks].T.astype(np.float16))
+    else:
+        yb = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.bfloat16)
+        assert np.array_equal(yb.float().cpu().numpy().view(np.uint32),
+                              np.ascontiguousarray(wref[:, ks].T).view(np.uint32))
 
 
 @pytest.mark.parametrize("odt,tol", [("bf16", 2.0 ** -8 + 2e-3), ("f16", 2.0 ** -11 + 2e-3)])
-@pytest.mark.parametrize("m", [33, 5])
+@pytest.mark.parametrize("m", [33, 5, 130, 300])
 def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
     torch = torch_dev
     n, k = 192, 2048
