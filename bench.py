@@ -642,9 +642,10 @@ def decode_3b(torch, tokens: int, warm: int, cpu_tokens: int, no_cpu: bool, pref
 
 def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     """The prefill-adjacency row: W4A16 GEMM X[M, K] @ W^T at the 8B gate shape
-    (14336 x 4096), fp16 activations, fp32 output, M in {1, 4, 16, 128, 512, 2048}: the
-    fused MFMA kernels of nve_hip_gemm_w4a16 (weight-streaming up to M = 192, 256 x 128
-    output tiles from M = 256)
+    (14336 x 4096), fp16 activations, fp32 output, M in {1, 4, 16, 128, 256, 512, 2048}:
+    the fused MFMA kernels of nve_hip_gemm_w4a16 (weight-streaming at M = 1-128 at this
+    shape, then the register-dequant tile kernel: 128-row tiles at M = 256, 256-row tiles
+    from M = 512)
     against the reference's own method on the same GPU
     (nve_dequant_w4a16 to fp16, then a dense fp16 GEMM -- torch.matmul, i.e. the
     vendor BLAS -- as GpuWeight::matmul_x does with candle, src/gpu_layer.rs:219-237).
@@ -656,7 +657,7 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     n, k = 14336, 4096
     nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
     out = {"shape": f"{n}x{k}", "x_dtype": "f16", "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS, "rows": []}
-    for m in (1, 4, 16, 128, 512, 2048):
+    for m in (1, 4, 16, 128, 256, 512, 2048):
         x = torch.randn((m, k), generator=g, device="cuda").half()
         wf = hk.dequant_w4(nib, sc, n, k)
 

@@ -760,16 +760,21 @@ static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const f
   }
 }
 
-constexpr int kGemmTileMinM = 256;
+constexpr int kGemmTileMinM = 128;
 
 hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
-  // from M = 256 (no AWQ, K % 128 == 0) the 256 x 128-tile kernel of gemm_w4a16_tile.hip
-  // (8B gate, fp16 out: 66.0 us at M = 256, 73.6 at 512, 149.8 at 1024, against 86.3 / 102.8
-  // / 218.3 us for the ring launches and the 128 x 128-tile kernel below)
-  if (M >= kGemmTileMinM && gemm_tile_fits(M, N, K, awq != nullptr))
+  // from M = 128 (no AWQ, K % 128 == 0) the 128- / 256-row tile kernel of
+  // gemm_w4a16_tile.hip, up to the ring launches' 320 rows only where its 128-row grid
+  // covers half the CUs: one workgroup streams all of K, so a narrow grid leaves the chip
+  // idle (fp16 out, us: 8B gate M = 192 / 256 51.2 / 51.4 against 72.0 / 95.5 for the ring
+  // launches; 8B down, 32 column tiles, M = 256: 133.8 against 120.9 for the ring; above
+  // 320 rows the tile kernel beats the 128 x 128-tile kernel below at both: gate M = 512
+  // 81.4 against 124.6, down 143 against 243)
+  if (M >= kGemmTileMinM && gemm_tile_fits(M, N, K, awq != nullptr) &&
+      (M > ring_chunked_max(false) || gemm_tile_grid128(M, N) >= 128))
     return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, out, out_dt, N, K, s);
   // up to M = 320 (AWQ: 128) where the ring fits: ring launches of up to 64 (AWQ: 32)
   // activation rows each (8B gate, 32-row launches: 27 us at M = 48 and about 58 us at 128, against

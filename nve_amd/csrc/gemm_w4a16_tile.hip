@@ -6,16 +6,18 @@
 // (f32 fma(n, s, -8 s) = (n - 8) s, then RNE to the activation type) but only in registers.
 //
 // Tile: 256 x 128 outputs per workgroup of 4 waves (2 x 2), 128 x 64 per wave as 4 x 2
-// tiles of v_mfma_f32_32x32x16; K advances 64 per slice (two Q4 blocks), two slices per
-// barrier (the barrier and each slice's first LDS reads cost about 450 cycles of a
-// 2,700-cycle slice).
+// tiles of v_mfma_f32_32x32x16, or 128 x 128 outputs as 4 waves (1 x 4) of 128 x 32 (4 x 1
+// tiles: each wave dequantizes only its own columns, and a given M has twice the
+// workgroups; the host takes it while that grid is one round); K advances 64 per slice
+// (two Q4 blocks), two slices per barrier (the barrier and each slice's first LDS reads
+// cost about 450 cycles of a 2,700-cycle slice).
 //   * Activation slices: global -> LDS transfers (buffer_load ... lds) one iteration ahead
 //     into two slots of two slices; the A operands are read from LDS (ds_read_b128).
 //   * Weights: the raw blocks (16 B of nibbles and the f32 scale per block row) go to a
 //     three-slot LDS ring two iterations ahead; each wave reads the 8-byte nibble runs of its
 //     64 rows once per slice and forms its B operands in registers (v_cvt_f32_ubyte, fma,
-//     v_cvt_pk), spread between its MFMAs.  The two waves sharing a column block both
-//     dequantize it; that VALU work runs beside the matrix pipe, while an LDS copy of the
+//     v_cvt_pk), spread between its MFMAs.  With 256-row tiles the two waves sharing a
+//     column block both dequantize it; that VALU work runs beside the matrix pipe, while an LDS copy of the
 //     dequantized weights would cost more LDS bandwidth than the MFMAs leave (measured:
 //     one ds_read_b128 per 32x32x16 MFMA already stretches it from 33 to 47 cycles).
 //   * One barrier per two slices.
@@ -33,13 +35,15 @@
 
 namespace nve {
 
-constexpr int TL_BM = 256, TL_BN = 128, TL_BK = 64;
-constexpr int TL_X = TL_BM * TL_BK * 2;  // 32 KiB: one 64-wide slice, 256 rows x 64 values
+// BM = 256 or 128 activation rows per tile; each wave owns 128 of them and BN / (4 / (BM /
+// 128)) columns: BM = 256 as 2 x 2 waves of 128 x 64, BM = 128 as 1 x 4 waves of 128 x 32
+constexpr int TL_BN = 128, TL_BK = 64;
+__host__ __device__ constexpr int tl_x_bytes(int bm) { return bm * TL_BK * 2; }  // one 64-wide slice
 constexpr int TL_R = TL_BN * 2 * 20;     // 5 KiB: one slice's 256 blocks x (16 B nibbles, 4 B scale)
 // An iteration (one barrier) covers two slices: two activation slots of two slices each,
-// three raw weight slots of two slices each
-constexpr int TL_R0 = 2 * 2 * TL_X;
-constexpr int TL_LDS = TL_R0 + 3 * 2 * TL_R;  // 158 KiB
+// three raw weight slots of two slices each (BM = 256: 158 KiB, 128: 94 KiB)
+__host__ __device__ constexpr int tl_r0(int bm) { return 2 * 2 * tl_x_bytes(bm); }
+__host__ __device__ constexpr int tl_lds_bytes(int bm) { return tl_r0(bm) + 3 * 2 * TL_R; }
 
 typedef _Float16 tl_h8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 tl_b8_t __attribute__((ext_vector_type(8)));
@@ -105,21 +109,26 @@ __device__ __forceinline__ u32x4_t tl_dequant8(uint32_t lo, uint32_t hi, float s
   return r;
 }
 
-template <bool BF16, int OUT_DT>
+template <bool BF16, int OUT_DT, int BM>
 __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t* __restrict__ x,
                                                                  const uint8_t* __restrict__ nib,
                                                                  const float* __restrict__ sc, void* __restrict__ out,
                                                                  int M, int N, int K, int n_tiles) {
   extern __shared__ __align__(16) char tl_lds[];
+  static_assert(BM == 256 || BM == 128, "row tile");
+  constexpr int WM = BM / 128;    // waves along M (each 128 rows)
+  constexpr int TJ = WM;          // 32-column MFMA tiles per wave: BN / (4 / WM) / 32
+  constexpr int NX = BM / 32;     // activation transfers (1 KiB) per wave and slice
+  constexpr int TL_X = tl_x_bytes(BM), TL_R0 = tl_r0(BM);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (4 / WM), wn = wave % (4 / WM);
 
   // XCD-grouped tile order: block b runs on XCD b % 8; the blocks of one XCD take
   // consecutive linear tiles (row block major)
   const int total = gridDim.x, b = blockIdx.x, xcd = b & 7;
   const int per = total >> 3, extra = total & 7;
   const int lin = xcd * per + min(xcd, extra) + (b >> 3);
-  const int m0 = (lin / n_tiles) * TL_BM, n0 = (lin % n_tiles) * TL_BN;
+  const int m0 = (lin / n_tiles) * BM, n0 = (lin % n_tiles) * TL_BN;
   const int T = K / TL_BK;
   const uint32_t lds0 = lds_addr(tl_lds);
 
@@ -128,13 +137,13 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc((void*)nib, (short)0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)sc, (short)0, 0x7fffffff, 0x00020000);
-  // activation transfers: instruction i of wave w fills tile rows 64 w + 8 i .. + 7 (1 KiB);
-  // lane l writes row 64 w + 8 i + l / 8 at chunk position l % 8, i.e. global chunk
-  // (l % 8) ^ ((row >> 1) & 7)
+  // activation transfers: instruction i of wave w fills tile rows (BM / 4) w + 8 i .. + 7
+  // (1 KiB); lane l writes row (BM / 4) w + 8 i + l / 8 at chunk position l % 8, i.e. global
+  // chunk (l % 8) ^ ((row >> 1) & 7)
   uint32_t xoff[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 64 * wave + 8 * i + (lane >> 3);
+  for (int i = 0; i < NX; ++i) {
+    const int r = (BM / 4) * wave + 8 * i + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     xoff[i] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + 8u * c) * 2u;
   }
@@ -151,11 +160,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   uint32_t koff[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) koff[kk] = ((2 * kk + fhi) ^ fsw) * 16;
-  // B operands: lane l of step kk takes row 64 wn + 32 j + l % 32, values 16 kk + 8 (l / 32)
+  // B operands: lane l of step kk takes row 32 (TJ wn + j) + l % 32, values 16 kk + 8 (l / 32)
   // .. + 7 of the slice = block kk / 2, nibble bytes 8 (l / 32) .. + 7, low nibbles for even
   // kk and high for odd: one 8-byte read per (j, block) serves two steps
-  const uint32_t bq = (uint32_t)(2 * (64 * wn + fr)) * 16 + 8 * fhi;  // + j * 1024 + block * 16
-  const uint32_t bs = 4096 + (uint32_t)(2 * (64 * wn + fr)) * 4;      // + j * 256 + block * 4
+  const uint32_t bq = (uint32_t)(2 * (32 * TJ * wn + fr)) * 16 + 8 * fhi;  // + j * 1024 + block * 16
+  const uint32_t bs = 4096 + (uint32_t)(2 * (32 * TJ * wn + fr)) * 4;      // + j * 256 + block * 4
 
   tl_f16x_t acc[4][2];
 #pragma unroll
@@ -174,12 +183,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   // activation transfers i0 .. i1 - 1 of slice t
   auto issue_x_part = [&](int t, int xslot, int i0, int i1) {
     const int ko = min(t, T - 1) * (TL_BK * 2);
-    char* const base = tl_lds + (2 * xslot + (t & 1)) * TL_X + wave * 64 * 128;
+    char* const base = tl_lds + (2 * xslot + (t & 1)) * TL_X + wave * (BM / 4) * 128;
 #pragma unroll
     for (int i = i0; i < i1; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(base + i * 1024), 16, xoff[i], ko, 0, 0);
   };
-  auto issue_x = [&](int t, int xslot) { issue_x_part(t, xslot, 0, 8); };  // slice t into its half of xslot
+  auto issue_x = [&](int t, int xslot) { issue_x_part(t, xslot, 0, NX); };  // slice t into its half of xslot
   auto rd_a = [&](uint32_t xa, int kk, u32x4_t (&fa)[4]) {
     const uint32_t a = xa + arow + koff[kk];
     fa[0] = tl_ds_read128<0>(a);
@@ -204,16 +213,18 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     u32x4_t fa[4];
     q[0][0] = tl_ds_read64<0>(rb + bq);
     q[0][1] = tl_ds_read64<16>(rb + bq);
-    q[1][0] = tl_ds_read64<1024>(rb + bq);
-    q[1][1] = tl_ds_read64<1040>(rb + bq);
     sbits[0][0] = tl_ds_read32<0>(rb + bs);
     sbits[0][1] = tl_ds_read32<4>(rb + bs);
-    sbits[1][0] = tl_ds_read32<256>(rb + bs);
-    sbits[1][1] = tl_ds_read32<260>(rb + bs);
+    if (TJ == 2) {
+      q[1][0] = tl_ds_read64<1024>(rb + bq);
+      q[1][1] = tl_ds_read64<1040>(rb + bq);
+      sbits[1][0] = tl_ds_read32<256>(rb + bs);
+      sbits[1][1] = tl_ds_read32<260>(rb + bs);
+    }
     rd_a(xa, 0, fa);
     lgkm_wait();
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         tie(q[j][h]);
@@ -221,12 +232,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
       }
     float s[2][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h) s[j][h] = __builtin_bit_cast(float, sbits[j][h]);
     u32x4_t fb[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j] = b_operand(q[j][0], s[j][0], 0);
+    for (int j = 0; j < TJ; ++j) fb[j] = b_operand(q[j][0], s[j][0], 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk > 0) lgkm_wait();
@@ -236,22 +247,22 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
 #pragma unroll
       for (int i = 0; i < 4; ++i) ca[i] = fa[i];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) cb[j] = fb[j];
+      for (int j = 0; j < TJ; ++j) cb[j] = fb[j];
       if (kk < 3) rd_a(xa, kk + 1, fa);
       iss(kk);
       // one scheduling region: the 8 MFMAs of step kk with the next step's B operands
       // formed between them
       if (kk < 3) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) fb[j] = b_operand(q[j][(kk + 1) >> 1], s[j][(kk + 1) >> 1], kk + 1);
+        for (int j = 0; j < TJ; ++j) fb[j] = b_operand(q[j][(kk + 1) >> 1], s[j][(kk + 1) >> 1], kk + 1);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = tl_mfma<BF16>(ca[i], cb[j], acc[i][j]);
+        for (int j = 0; j < TJ; ++j) acc[i][j] = tl_mfma<BF16>(ca[i], cb[j], acc[i][j]);
       if (kk < 3) {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
+        for (int m = 0; m < 4 * TJ; ++m) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
         }
@@ -284,7 +295,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t xa = lds0 + 2 * xs * TL_X, rb = lds0 + TL_R0 + 2 * rs * TL_R;
     mma(xa, rb, [&](int kk) {
-      issue_x_part(t + 2 + (kk >> 1), xs ^ 1, 4 * (kk & 1), 4 * (kk & 1) + 4);
+      issue_x_part(t + 2 + (kk >> 1), xs ^ 1, (NX / 2) * (kk & 1), (NX / 2) * (kk & 1) + NX / 2);
     });
     mma(xa + TL_X, rb + TL_R, [&](int kk) {
       if (kk == 0) issue_raw(t + 4, rs2);
@@ -302,8 +313,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 64 * wn + 32 * j + fr;
+    for (int j = 0; j < TJ; ++j) {
+      const int n = n0 + 32 * (TJ * wn + j) + fr;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * fhi + (r & 3);
@@ -319,26 +330,41 @@ namespace nve_host {
 // The tile kernel serves K % 128 == 0 (two slices per iteration) without AWQ, where every
 // byte offset fits its buffer resource (2^31 - 1 bytes; reads past it would return zeros):
 // activations M K, nibbles N K / 2 and scales N K / 8 bytes.
+long gemm_tile_grid128(int M, int N) {
+  return (long)((M + 127) / 128) * ((N + nve::TL_BN - 1) / nve::TL_BN);
+}
+
 bool gemm_tile_fits(int M, int N, int K, bool awq) {
   return !awq && K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30) && (long)N * (K / 2) < (1L << 31);
 }
 
-template <bool BF16, int OUT_DT>
-static hipError_t launch_tile_t(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
-                                hipStream_t s) {
-  auto kern = nve::gemm_w4a16_tile_kernel<BF16, OUT_DT>;
+template <bool BF16, int OUT_DT, int BM>
+static hipError_t launch_tile_bm(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
+                                 hipStream_t s) {
+  auto kern = nve::gemm_w4a16_tile_kernel<BF16, OUT_DT, BM>;
+  constexpr int lds = nve::tl_lds_bytes(BM);
   static thread_local int attr_dev = -1;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (attr_dev != dev) {
-    e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, nve::TL_LDS);
+    e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     attr_dev = dev;
   }
-  const int nt = (N + nve::TL_BN - 1) / nve::TL_BN, mt = (M + nve::TL_BM - 1) / nve::TL_BM;
-  hipLaunchKernelGGL(kern, dim3(nt * mt), dim3(256), nve::TL_LDS, s, (const uint16_t*)x, nib, sc, out, M, N, K, nt);
+  const int nt = (N + nve::TL_BN - 1) / nve::TL_BN, mt = (M + BM - 1) / BM;
+  hipLaunchKernelGGL(kern, dim3(nt * mt), dim3(256), lds, s, (const uint16_t*)x, nib, sc, out, M, N, K, nt);
   return hipGetLastError();
+}
+
+// 128-row tiles while their grid is one round (at most one workgroup per CU), else 256
+// (8B gate, fp16 out, us: M = 256 51.4 against 71.2 with 256-row tiles; M = 512 103.3
+// against 81.4, the 128-row grid there being 448 workgroups)
+template <bool BF16, int OUT_DT>
+static hipError_t launch_tile_t(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
+                                hipStream_t s) {
+  if (gemm_tile_grid128(M, N) <= 256) return launch_tile_bm<BF16, OUT_DT, 128>(x, M, nib, sc, out, N, K, s);
+  return launch_tile_bm<BF16, OUT_DT, 256>(x, M, nib, sc, out, N, K, s);
 }
 
 hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, void* out,

@@ -219,8 +219,10 @@ hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W
                              hipStream_t stream, const nve::EpiArgs& ra);
 hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                               hipStream_t stream, const nve::EpiArgs& ra);
-// Large-M W4A16 GEMM (gemm_w4a16_tile.hip): K % 64 == 0, no AWQ, M K < 2^30.
+// Large-M W4A16 GEMM (gemm_w4a16_tile.hip): K % 128 == 0, no AWQ, M K < 2^30,
+// N K / 2 < 2^31; gemm_tile_grid128 = its workgroup count with 128-row tiles.
 bool gemm_tile_fits(int M, int N, int K, bool awq);
+long gemm_tile_grid128(int M, int N);
 hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, void* out,
                                   int out_dt, int N, int K, hipStream_t s);
 hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, int vocab, hipStream_t s);

@@ -45,7 +45,8 @@ def _round(a, dt):
                                    (24, 14336, 4096), (32, 4096, 14336), (20, 300, 256), (48, 14336, 4096),
                                    (100, 2000, 1024), (48, 16400, 512), (33, 200, 4160), (64, 14336, 4096), (60, 300, 512), (320, 1000, 1024), (129, 700, 512),
                                    (17, 96, 1024), (32, 520, 1024), (33, 300, 2048), (128, 128, 1024), (200, 520, 3072), (512, 256, 8192),
-                                   (300, 1000, 512), (600, 520, 2048), (1100, 300, 1024)])
+                                   (300, 1000, 512), (600, 520, 2048), (1100, 300, 1024), (200, 8192, 1024),
+                                   (520, 8300, 512)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_parity(orc, torch_dev, hk, m, n, k, xdt, with_awq):
@@ -115,17 +116,20 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
     assert np.array_equal(got.T.view(np.uint32), wref.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 130, 256), (300, 1000, 512), (257, 129, 256), (1100, 300, 1024), (300, 200, 192)])
+@pytest.mark.parametrize("m,n,k", [(330, 130, 256), (321, 1000, 512), (130, 16000, 256), (1100, 300, 1024),
+                                   (600, 8200, 256), (513, 4100, 512), (300, 200, 192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n, k, xdt):
-    """From M = 256 without AWQ and with K % 128 == 0 the 256 x 128-tile kernel runs
-    (gemm_w4a16_tile.hip; K % 128 == 64, here K = 192, the 128 x 128-tile kernel).
-    One-hot activation rows (row i picks column k_i) make each output one product
-    1 * w, so Y[i, :] is weight column k_i as the kernel rounded it, which must equal the
-    reference dequant bit for bit.  Ragged M and N, K = 256 (one iteration of two
-    slices), and tile grids that are not a multiple of 8 workgroups (the XCD-grouped
-    tile order: 2 x 2, 2 x 8, 2 x 2 and 5 x 3 tiles); fp32 output, and fp16 / bf16 output
-    for fp16 / bf16 x (exact too)."""
+    """Without AWQ and with K % 128 == 0 the tile kernel (gemm_w4a16_tile.hip) runs above
+    320 rows, and from 128 rows where its 128-row grid has at least 128 workgroups; it
+    takes 128-row tiles while that grid has at most 256 workgroups, else 256-row tiles
+    (here: 128 rows at 3 x 2, 3 x 8, 2 x 125, 9 x 3 and 5 x 33 tiles, 256 rows at 3 x 65;
+    K % 128 == 64, here K = 192, runs the 128 x 128-tile kernel).  One-hot activation rows
+    (row i picks column k_i) make each output one product 1 * w, so Y[i, :] is weight
+    column k_i as the kernel rounded it, which must equal the reference dequant bit for
+    bit.  Ragged M and N, K = 256 (one iteration of two slices), and tile grids that are
+    not a multiple of 8 workgroups (the XCD-grouped tile order); fp32 output, and fp16 /
+    bf16 output for fp16 / bf16 x (exact too)."""
     torch = torch_dev
     print(f"tile identity m={m} n={n} k={k} x={xdt}", flush=True)
     data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.3))
