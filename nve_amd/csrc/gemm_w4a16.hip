@@ -630,6 +630,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 namespace nve_host {
 
 constexpr int kGemmSmallM = 16;
+constexpr int kGemmTileMinM = 128;  // the register-dequant tile kernel's first M
 constexpr int kSmallKS = 16;
 
 // K splits of the tiled kernel: split while the tile grid covers fewer than 512
@@ -643,10 +644,13 @@ static int gemm_split(int M, int N, int K, int out_dt) {
   return split;
 }
 
-// Bytes of fp32 partials the bit-reproducible split needs (0: no split).
+// Bytes of fp32 partials the bit-reproducible splits need (0: no split): that of this
+// file's tiled kernel or that of the register-dequant tile kernel, whichever is larger.
 size_t gemm_split_parts_bytes(int M, int N, int K) {
   const int split = gemm_split(M, N, K, NVE_DT_F32);
-  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+  const size_t own = split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+  const size_t tile = M >= kGemmTileMinM ? gemm_tile_parts_bytes(M, N, K) : 0;
+  return own > tile ? own : tile;
 }
 
 // parts (parts_bytes >= gemm_split_parts_bytes): a split launch stores its partials
@@ -760,22 +764,24 @@ static hipError_t launch_small(const void* x, int M, const uint8_t* nib, const f
   }
 }
 
-constexpr int kGemmTileMinM = 128;
-
 hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
   // from M = 128 (no AWQ, K % 128 == 0) the 128- / 256-row tile kernel of
-  // gemm_w4a16_tile.hip, up to the ring launches' 320 rows only where its 128-row grid
-  // covers half the CUs: one workgroup streams all of K, so a narrow grid leaves the chip
-  // idle (fp16 out, us: 8B gate M = 192 / 256 51.2 / 51.4 against 72.0 / 95.5 for the ring
-  // launches; 8B down, 32 column tiles, M = 256: 133.8 against 120.9 for the ring; above
-  // 320 rows the tile kernel beats the 128 x 128-tile kernel below at both: gate M = 512
-  // 81.4 against 124.6, down 143 against 243)
-  if (M >= kGemmTileMinM && gemm_tile_fits(M, N, K, awq != nullptr) &&
-      (M > ring_chunked_max(false) || gemm_tile_grid128(M, N) >= 128))
-    return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, out, out_dt, N, K, s);
+  // gemm_w4a16_tile.hip.  Without room for K-split partials it runs up to the ring
+  // launches' 320 rows only where its 128-row grid covers half the CUs: one workgroup
+  // streams all of K, so a narrow grid leaves the chip idle (fp16 out, us: 8B gate M = 192
+  // / 256 51.2 / 51.4 against 72.0 / 95.5 for the ring launches; 8B down, 32 column tiles,
+  // M = 256: 133.8 against 120.9 for the ring; above 320 rows the tile kernel beats the
+  // 128 x 128-tile kernel below at both: gate M = 512 81.4 against 124.6, down 143 against
+  // 243).  With the partials a narrow grid is split over K instead.
+  if (M >= kGemmTileMinM && gemm_tile_fits(M, N, K, awq != nullptr)) {
+    const size_t tp = gemm_tile_parts_bytes(M, N, K);
+    const bool split = parts && tp > 0 && parts_bytes >= tp;
+    if (split || M > ring_chunked_max(false) || gemm_tile_grid128(M, N) >= 128)
+      return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, out, out_dt, N, K, split ? parts : nullptr, parts_bytes, s);
+  }
   // up to M = 320 (AWQ: 128) where the ring fits: ring launches of up to 64 (AWQ: 32)
   // activation rows each (8B gate, 32-row launches: 27 us at M = 48 and about 58 us at 128, against
   // 45 / 71 us for the tiled kernel); a row's result does not depend on the rows

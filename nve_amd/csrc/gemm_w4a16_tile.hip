@@ -109,11 +109,14 @@ __device__ __forceinline__ u32x4_t tl_dequant8(uint32_t lo, uint32_t hi, float s
   return r;
 }
 
-template <bool BF16, int OUT_DT, int BM>
+// SPLIT: blockIdx.y = z takes slices z ks .. z ks + ks - 1 of K (ks even) and stores its
+// fp32 partial tile to out + z M N (tl_reduce_kernel adds the partials in order).
+template <bool BF16, int OUT_DT, int BM, bool SPLIT>
 __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t* __restrict__ x,
                                                                  const uint8_t* __restrict__ nib,
                                                                  const float* __restrict__ sc, void* __restrict__ out,
-                                                                 int M, int N, int K, int n_tiles) {
+                                                                 int M, int N, int K, int n_tiles, int ks) {
+  static_assert(!SPLIT || OUT_DT == NVE_DT_F32, "split partials are fp32");
   extern __shared__ __align__(16) char tl_lds[];
   static_assert(BM == 256 || BM == 128, "row tile");
   constexpr int WM = BM / 128;    // waves along M (each 128 rows)
@@ -129,7 +132,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   const int per = total >> 3, extra = total & 7;
   const int lin = xcd * per + min(xcd, extra) + (b >> 3);
   const int m0 = (lin / n_tiles) * BM, n0 = (lin % n_tiles) * TL_BN;
-  const int T = K / TL_BK;
+  // this workgroup's slices: t0 .. t0 + T - 1
+  const int t0 = SPLIT ? (int)blockIdx.y * ks : 0;
+  const int T = SPLIT ? min(K / TL_BK - t0, ks) : K / TL_BK;
   const uint32_t lds0 = lds_addr(tl_lds);
 
   // buffer resources (raw buffers, 32-bit offsets: the host routes M K >= 2^30
@@ -175,14 +180,14 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   // transfers of slice t (clamped to the last slice: the ones past the end re-read it,
   // which keeps every iteration's transfer count equal)
   auto issue_raw = [&](int t, int rslot) {
-    const int tc = min(t, T - 1);
+    const int tc = t0 + min(t, T - 1);
     char* const rb = tl_lds + TL_R0 + (2 * rslot + (t & 1)) * TL_R;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(nr, (lds_void_t*)(rb + wave * 1024), 16, noff, tc * 32, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void_t*)(rb + 4096 + wave * 256), 4, soff, tc * 8, 0, 0);
   };
   // activation transfers i0 .. i1 - 1 of slice t
   auto issue_x_part = [&](int t, int xslot, int i0, int i1) {
-    const int ko = min(t, T - 1) * (TL_BK * 2);
+    const int ko = (t0 + min(t, T - 1)) * (TL_BK * 2);
     char* const base = tl_lds + (2 * xslot + (t & 1)) * TL_X + wave * (BM / 4) * 128;
 #pragma unroll
     for (int i = i0; i < i1; ++i)
@@ -318,9 +323,25 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * fhi + (r & 3);
-        if (m < M && n < N) store_out<OUT_DT>(out, (size_t)m * N + n, acc[i][j][r]);
+        if (m < M && n < N) {
+          if constexpr (SPLIT)
+            ((float*)out)[(size_t)blockIdx.y * M * N + (size_t)m * N + n] = acc[i][j][r];
+          else
+            store_out<OUT_DT>(out, (size_t)m * N + n, acc[i][j][r]);
+        }
       }
     }
+}
+
+// out[i] = sum over z = 0 .. split - 1 of part[z n + i], in that order, rounded to OUT_DT
+template <int OUT_DT>
+__global__ __launch_bounds__(256) void tl_reduce_kernel(const float* __restrict__ part, void* __restrict__ out,
+                                                        size_t n, int split) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float y = part[i];
+  for (int z = 1; z < split; ++z) y += part[(size_t)z * n + i];
+  store_out<OUT_DT>(out, i, y);
 }
 
 }  // namespace nve
@@ -334,14 +355,33 @@ long gemm_tile_grid128(int M, int N) {
   return (long)((M + 127) / 128) * ((N + nve::TL_BN - 1) / nve::TL_BN);
 }
 
+// K split of a 128-row tile grid that leaves CUs idle: as many splits as keep the grid
+// within one round (256 workgroups) and at least 4 iterations (8 slices) each; *ks =
+// slices per split (even), and the returned count has no empty split.
+static int tile_split(int M, int N, int K, int* ks) {
+  const long g = gemm_tile_grid128(M, N);
+  const int kit = K / (2 * nve::TL_BK);
+  const int by_grid = g >= 256 ? 1 : (int)(256 / g), by_k = kit / 4 > 1 ? kit / 4 : 1;
+  const int split = by_grid < by_k ? by_grid : by_k;
+  const int per = 2 * ((kit + split - 1) / split);
+  if (ks) *ks = per;
+  return (2 * kit + per - 1) / per;
+}
+
+size_t gemm_tile_parts_bytes(int M, int N, int K) {
+  if (!gemm_tile_fits(M, N, K, false)) return 0;
+  const int split = tile_split(M, N, K, nullptr);
+  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+}
+
 bool gemm_tile_fits(int M, int N, int K, bool awq) {
   return !awq && K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30) && (long)N * (K / 2) < (1L << 31);
 }
 
-template <bool BF16, int OUT_DT, int BM>
+template <bool BF16, int OUT_DT, int BM, bool SPLIT = false>
 static hipError_t launch_tile_bm(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
-                                 hipStream_t s) {
-  auto kern = nve::gemm_w4a16_tile_kernel<BF16, OUT_DT, BM>;
+                                 hipStream_t s, int split = 1, int ks = 0) {
+  auto kern = nve::gemm_w4a16_tile_kernel<BF16, OUT_DT, BM, SPLIT>;
   constexpr int lds = nve::tl_lds_bytes(BM);
   static thread_local int attr_dev = -1;
   int dev = 0;
@@ -353,7 +393,7 @@ static hipError_t launch_tile_bm(const void* x, int M, const uint8_t* nib, const
     attr_dev = dev;
   }
   const int nt = (N + nve::TL_BN - 1) / nve::TL_BN, mt = (M + BM - 1) / BM;
-  hipLaunchKernelGGL(kern, dim3(nt * mt), dim3(256), lds, s, (const uint16_t*)x, nib, sc, out, M, N, K, nt);
+  hipLaunchKernelGGL(kern, dim3(nt * mt, split), dim3(256), lds, s, (const uint16_t*)x, nib, sc, out, M, N, K, nt, ks);
   return hipGetLastError();
 }
 
@@ -367,10 +407,34 @@ static hipError_t launch_tile_t(const void* x, int M, const uint8_t* nib, const 
   return launch_tile_bm<BF16, OUT_DT, 256>(x, M, nib, sc, out, N, K, s);
 }
 
+// With parts (parts_bytes >= gemm_tile_parts_bytes) a small grid is split over K: fp32
+// partials there, added in a fixed order and rounded to out_dt by a second launch.
+template <bool BF16>
+static hipError_t launch_tile_split(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int out_dt,
+                                   int N, int K, float* parts, int split, int ks, hipStream_t s) {
+  hipError_t e = launch_tile_bm<BF16, NVE_DT_F32, 128, true>(x, M, nib, sc, parts, N, K, s, split, ks);
+  if (e != hipSuccess) return e;
+  const size_t n = (size_t)M * N;
+  const dim3 g((unsigned)((n + 255) / 256));
+  switch (out_dt) {
+    case NVE_DT_F16: hipLaunchKernelGGL(nve::tl_reduce_kernel<NVE_DT_F16>, g, dim3(256), 0, s, parts, out, n, split); break;
+    case NVE_DT_BF16: hipLaunchKernelGGL(nve::tl_reduce_kernel<NVE_DT_BF16>, g, dim3(256), 0, s, parts, out, n, split); break;
+    default: hipLaunchKernelGGL(nve::tl_reduce_kernel<NVE_DT_F32>, g, dim3(256), 0, s, parts, out, n, split); break;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, void* out,
-                                  int out_dt, int N, int K, hipStream_t s) {
+                                  int out_dt, int N, int K, float* parts, size_t parts_bytes, hipStream_t s) {
   if (K % (2 * nve::TL_BK) != 0) return hipErrorInvalidValue;
   const bool bf = x_dt == NVE_DT_BF16;
+  if (parts) {
+    int ks = 0;
+    const int split = tile_split(M, N, K, &ks);
+    if (split > 1 && parts_bytes >= (size_t)split * M * N * sizeof(float))
+      return bf ? launch_tile_split<true>(x, M, nib, sc, out, out_dt, N, K, parts, split, ks, s)
+                : launch_tile_split<false>(x, M, nib, sc, out, out_dt, N, K, parts, split, ks, s);
+  }
 #define NVE_TL(B)                                                                       \
   switch (out_dt) {                                                                     \
     case NVE_DT_F16: return launch_tile_t<B, NVE_DT_F16>(x, M, nib, sc, out, N, K, s);   \

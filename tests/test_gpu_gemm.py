@@ -225,7 +225,8 @@ def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
 
 def test_gemm_w4a16_ws_graph_capture(orc, torch_dev, hk):
     """Under HIP graph capture: a shape first seen during capture takes the fused kernel
-    (no handle creation or timing in the graph); after an eager call has selected the
+    (no handle creation or timing in the graph; with the workspace's K-split partials,
+    as an eager call whose workspace only fits those); after an eager call has selected the
     algorithm, the captured graph replays the BLAS path.  Every replay matches eager."""
     torch = torch_dev
     # N = 544 is used by no other test: the algorithm cache is process-wide, so the cold
@@ -238,7 +239,10 @@ def test_gemm_w4a16_ws_graph_capture(orc, torch_dev, hk):
         x = torch.randn((m, k), device="cuda").to(torch.float16)
         ws = torch.empty(hk.gemm_w4a16_workspace_bytes(m, n, k), dtype=torch.uint8, device="cuda")
         out = torch.empty((m, n), dtype=torch.float16, device="cuda")
-        eager_fused = hk.gemm_w4a16(x, nib, sc, n, k, out_dtype=torch.float16)
+        # the fused path with this workspace (K-split partials): a workspace slice too
+        # small for the BLAS path but large enough for the partials
+        assert m * n * 32 < n * k * 2 + (32 << 20)
+        eager_fused = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws[: m * n * 32], out_dtype=torch.float16)
         if warm:
             eager = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16)
         torch.cuda.synchronize()
@@ -291,6 +295,55 @@ def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
     wref = _round(orc.q4_to_f32(data, n, k, None), "f16").astype(np.float64)
     ref = xh.astype(np.float64) @ wref.T
     assert rel_err_floor(a.cpu().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("m,n,k", [(200, 520, 2048), (300, 1000, 1152), (130, 4100, 8192), (513, 300, 1024)])
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_gemm_w4a16_ws_tile_split(orc, torch_dev, hk, m, n, k, xdt):
+    """With a workspace, the register-dequant tile kernel splits K where its 128-row grid
+    leaves CUs idle (here 2 x 5 tiles in 4 splits, 3 x 8 in 2 of 10 and 8 slices, 2 x 33 in
+    3 of 44, 44 and 40, 5 x 3 in 2; M = 513 takes the fused path when the output type is neither fp32 nor
+    x's): each split stores fp32 partials, one more launch adds them in split order and
+    rounds once to the output type.  Every call and every graph replay gives the same
+    bits; an fp16 / bf16 output is exactly the fp32 result rounded; the product is within
+    fp32 rounding of the unsplit one and within the W4A16 bar of the oracle."""
+    torch = torch_dev
+    print(f"tile split m={m} n={n} k={k} x={xdt}", flush=True)
+    wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
+    assert wsb >= 2 * m * n * 4
+    data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.05))
+    nib_h, sc_h = orc.extract_for_gpu(data, n, k)
+    nib, sc = torch.from_numpy(nib_h).cuda(), torch.from_numpy(sc_h).cuda()
+    xr = _round(np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32), xdt)
+    tdt = torch.float16 if xdt == "f16" else torch.bfloat16
+    x = torch.from_numpy(xr).cuda().to(tdt)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    if m <= 512:
+        a = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
+        assert torch.equal(a, hk.gemm_w4a16_ws(x, nib, sc, n, k, ws))
+        unsplit = hk.gemm_w4a16(x, nib, sc, n, k)
+        assert torch.allclose(a, unsplit, rtol=1e-5, atol=1e-5 * float(a.abs().max()))
+        wref = _round(orc.q4_to_f32(data, n, k, None), xdt).astype(np.float64)
+        assert rel_err_floor(a.cpu().numpy(), xr.astype(np.float64) @ wref.T) <= 2e-3
+        for odt in (torch.float16, torch.bfloat16):
+            assert torch.equal(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=odt), a.to(odt))
+    else:
+        odt = torch.bfloat16 if xdt == "f16" else torch.float16  # not BLAS-eligible: fused
+        a = hk.gemm_w4a16(x, nib, sc, n, k).to(odt)
+        b = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=odt)
+        assert torch.allclose(a.float(), b.float(), rtol=2 ** -7, atol=1e-5 * float(a.float().abs().max()))
+    out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    ref16 = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out.copy_(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16))
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref16)
 
 
 @pytest.mark.parametrize("m", [8, 48, 200])
