@@ -630,7 +630,13 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 namespace nve_host {
 
 constexpr int kGemmSmallM = 16;
-constexpr int kGemmTileMinM = 128;  // the register-dequant tile kernel's first M
+// the register-dequant tile kernel's first M: without K-split partials, and with them
+// (from the first M the ring takes in two launches; workspace path, fp32 out, us: 8B gate
+// M = 80 / 96 / 112 32.5 / 32.9 / 33.4 against 35.8 / 37.7 / 43.8 for the ring launches,
+// 8B down 29.8 / 30.0 / 31.2 against 39.8 / 45.8 / 54.4; at M = 64, one ring launch, 31.5
+// / 28.9 against 24.1 / 28.3)
+constexpr int kGemmTileMinM = 128;
+constexpr int kGemmTileSplitMinM = 65;
 constexpr int kSmallKS = 16;
 
 // K splits of the tiled kernel: split while the tile grid covers fewer than 512
@@ -649,7 +655,7 @@ static int gemm_split(int M, int N, int K, int out_dt) {
 size_t gemm_split_parts_bytes(int M, int N, int K) {
   const int split = gemm_split(M, N, K, NVE_DT_F32);
   const size_t own = split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
-  const size_t tile = M >= kGemmTileMinM ? gemm_tile_parts_bytes(M, N, K) : 0;
+  const size_t tile = M >= kGemmTileSplitMinM ? gemm_tile_parts_bytes(M, N, K) : 0;
   return own > tile ? own : tile;
 }
 
@@ -769,17 +775,17 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
   // from M = 128 (no AWQ, K % 128 == 0) the 128- / 256-row tile kernel of
-  // gemm_w4a16_tile.hip.  Without room for K-split partials it runs up to the ring
+  // gemm_w4a16_tile.hip; with K-split partials from M = 65.  Without them it runs up to the ring
   // launches' 320 rows only where its 128-row grid covers half the CUs: one workgroup
   // streams all of K, so a narrow grid leaves the chip idle (fp16 out, us: 8B gate M = 192
   // / 256 51.2 / 51.4 against 72.0 / 95.5 for the ring launches; 8B down, 32 column tiles,
   // M = 256: 133.8 against 120.9 for the ring; above 320 rows the tile kernel beats the
   // 128 x 128-tile kernel below at both: gate M = 512 81.4 against 124.6, down 143 against
   // 243).  With the partials a narrow grid is split over K instead.
-  if (M >= kGemmTileMinM && gemm_tile_fits(M, N, K, awq != nullptr)) {
+  if (M >= kGemmTileSplitMinM && gemm_tile_fits(M, N, K, awq != nullptr)) {
     const size_t tp = gemm_tile_parts_bytes(M, N, K);
     const bool split = parts && tp > 0 && parts_bytes >= tp;
-    if (split || M > ring_chunked_max(false) || gemm_tile_grid128(M, N) >= 128)
+    if (split || (M >= kGemmTileMinM && (M > ring_chunked_max(false) || gemm_tile_grid128(M, N) >= 128)))
       return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, out, out_dt, N, K, split ? parts : nullptr, parts_bytes, s);
   }
   // up to M = 320 (AWQ: 128) where the ring fits: ring launches of up to 64 (AWQ: 32)
