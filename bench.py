@@ -727,6 +727,25 @@ def prefill_probe(torch, hk):
     print(json.dumps({"probe": "prefill", "shape": f"{n}x{k}", "M": [512, 2048], "launches_each": 5}), flush=True)
 
 
+def prefill_ws_probe(torch, hk):
+    """Eager launches of nve_hip_gemm_w4a16_ws (fp16 x, fp32 out, with its workspace) for
+    a rocprofv3 kernel trace of the K-split tile path: the 8B gate (14336x4096) and down
+    (4096x14336) shapes at M = 96, 128, 256, 512, one warm-up then 5 launches each."""
+    g = torch.Generator(device="cuda").manual_seed(17)
+    cases = []
+    for n, k in ((14336, 4096), (4096, 14336)):
+        nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
+        for m in (96, 128, 256, 512):
+            x = torch.randn((m, k), generator=g, device="cuda").half()
+            ws = torch.empty(hk.gemm_w4a16_workspace_bytes(m, n, k), dtype=torch.uint8, device="cuda")
+            for _ in range(6):
+                hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
+            torch.cuda.synchronize()
+            cases.append({"N": n, "K": k, "M": m, "workspace_bytes": ws.numel()})
+            del x, ws
+    print(json.dumps({"probe": "prefill_ws", "launches_each": 6, "cases": cases}), flush=True)
+
+
 def batched_probe(torch, L, hk):
     """Short eager run for rocprofv3 --pmc of the batched W4A8 kernels (MFMA counters):
     the configs[3] shapes (8B gate and down) at M in {1, 2, 4, 8, 16}, 10 launches each
@@ -839,6 +858,9 @@ def main():
     ap.add_argument("--suite-probe", action="store_true",
                     help="only the per-shape 8B table and the batched sweep, for rocprofv3 --kernel-trace "
                          "per-shape kernel durations (no bench line)")
+    ap.add_argument("--prefill-ws-probe", action="store_true",
+                    help="eager nve_hip_gemm_w4a16_ws launches (8B gate / down, M = 96-512) for a rocprofv3 "
+                         "kernel trace of the K-split tile path (no bench line)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="eager fused prefill GEMM launches at M = 512 / 2048 for rocprofv3 --pmc (no bench line)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -870,6 +892,9 @@ def main():
         return
     if args.suite_probe:
         suite_probe(torch, L, hk)
+        return
+    if args.prefill_ws_probe:
+        prefill_ws_probe(torch, hk)
         return
     if args.prefill_probe:
         prefill_probe(torch, hk)
