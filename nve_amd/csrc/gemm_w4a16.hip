@@ -775,18 +775,22 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
   // from M = 128 (no AWQ, K % 128 == 0) the 128- / 256-row tile kernel of
-  // gemm_w4a16_tile.hip; with K-split partials from M = 65.  Without them it runs up to the ring
-  // launches' 320 rows only where its 128-row grid covers half the CUs: one workgroup
-  // streams all of K, so a narrow grid leaves the chip idle (fp16 out, us: 8B gate M = 192
-  // / 256 51.2 / 51.4 against 72.0 / 95.5 for the ring launches; 8B down, 32 column tiles,
-  // M = 256: 133.8 against 120.9 for the ring; above 320 rows the tile kernel beats the
-  // 128 x 128-tile kernel below at both: gate M = 512 81.4 against 124.6, down 143 against
+  // gemm_w4a16_tile.hip (with AWQ from M = 65); with K-split partials from M = 65.  Without
+  // them it runs up to the ring launches' range (320 rows, AWQ 128) only where its 128-row
+  // grid has at least 96 workgroups: one workgroup streams all of K, so a narrow grid
+  // leaves the chip idle (fp16 out, us: 8B gate M = 128 / 192 / 256 45.5 / 51.2 / 51.4
+  // against 47.9 / 72.0 / 95.5 for the ring launches; 8B down, 32 column tiles, M = 256:
+  // 133.8 against 120.9 for the ring; above that range the tile kernel beats the 128 x
+  // 128-tile kernel below at both: gate M = 512 81.4 against 124.6, down 143 against
   // 243).  With the partials a narrow grid is split over K instead.
   if (M >= kGemmTileSplitMinM && gemm_tile_fits(M, N, K, awq != nullptr)) {
     const size_t tp = gemm_tile_parts_bytes(M, N, K);
     const bool split = parts && tp > 0 && parts_bytes >= tp;
-    if (split || (M >= kGemmTileMinM && (M > ring_chunked_max(false) || gemm_tile_grid128(M, N) >= 128)))
-      return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, out, out_dt, N, K, split ? parts : nullptr, parts_bytes, s);
+    // (AWQ: from M = 65, where the 32-row ring launches number three or more)
+    const int tile_min = awq ? kGemmTileSplitMinM : kGemmTileMinM;
+    if (split || M > ring_chunked_max(awq != nullptr) || (M >= tile_min && gemm_tile_grid128(M, N) >= 96))
+      return launch_gemm_w4a16_tile(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, split ? parts : nullptr,
+                                    parts_bytes, s);
   }
   // up to M = 320 (AWQ: 128) where the ring fits: ring launches of up to 64 (AWQ: 32)
   // activation rows each (8B gate, 32-row launches: 27 us at M = 48 and about 58 us at 128, against

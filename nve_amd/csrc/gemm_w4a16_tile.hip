@@ -39,11 +39,13 @@ namespace nve {
 // 128)) columns: BM = 256 as 2 x 2 waves of 128 x 64, BM = 128 as 1 x 4 waves of 128 x 32
 constexpr int TL_BN = 128, TL_BK = 64;
 __host__ __device__ constexpr int tl_x_bytes(int bm) { return bm * TL_BK * 2; }  // one 64-wide slice
-constexpr int TL_R = TL_BN * 2 * 20;     // 5 KiB: one slice's 256 blocks x (16 B nibbles, 4 B scale)
+// raw weights of one slice: 256 blocks x (16 B nibbles, 4 B scale) = 5 KiB, and with AWQ the
+// slice's 64 factors (256 B) after them
+__host__ __device__ constexpr int tl_r_bytes(bool awq) { return TL_BN * 2 * 20 + (awq ? 256 : 0); }
 // An iteration (one barrier) covers two slices: two activation slots of two slices each,
-// three raw weight slots of two slices each (BM = 256: 158 KiB, 128: 94 KiB)
+// three raw weight slots of two slices each (BM = 256: 158 KiB, 159.5 with AWQ; 128: 94 KiB)
 __host__ __device__ constexpr int tl_r0(int bm) { return 2 * 2 * tl_x_bytes(bm); }
-__host__ __device__ constexpr int tl_lds_bytes(int bm) { return tl_r0(bm) + 3 * 2 * TL_R; }
+__host__ __device__ constexpr int tl_lds_bytes(int bm, bool awq) { return tl_r0(bm) + 3 * 2 * tl_r_bytes(awq); }
 
 typedef _Float16 tl_h8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 tl_b8_t __attribute__((ext_vector_type(8)));
@@ -89,9 +91,12 @@ __device__ __forceinline__ uint32_t tl_pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((tl_f2_t){a, b}, tl_h2_t));
 }
 // The reference dequant of 8 nibbles -- one per byte of lo (values 0..3) and hi (values
-// 4..7), already masked -- rounded to the activation type and packed in k order.
-template <bool BF16>
-__device__ __forceinline__ u32x4_t tl_dequant8(uint32_t lo, uint32_t hi, float s, float s8) {
+// 4..7), already masked -- [times the AWQ factors a0 (values 0..3) and a1 (4..7), each an
+// f32 product of the f32 dequantized value as the reference forms it,] rounded to the
+// activation type and packed in k order.
+template <bool BF16, bool AWQ>
+__device__ __forceinline__ u32x4_t tl_dequant8(uint32_t lo, uint32_t hi, float s, float s8, const u32x4_t& a0,
+                                               const u32x4_t& a1) {
   // the masked dwords are opaque to the compiler, so each byte goes through one
   // v_cvt_f32_ubyte{0..3} (instead of a bit-field extract and a conversion)
   asm("" : "+v"(lo), "+v"(hi));
@@ -100,6 +105,11 @@ __device__ __forceinline__ u32x4_t tl_dequant8(uint32_t lo, uint32_t hi, float s
   for (int t = 0; t < 4; ++t) {
     v[t] = fmaf((float)((lo >> (8 * t)) & 0xffu), s, s8);
     v[4 + t] = fmaf((float)((hi >> (8 * t)) & 0xffu), s, s8);
+  }
+  if constexpr (AWQ) {
+    const uint32_t f[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] *= __builtin_bit_cast(float, f[e]);
   }
   u32x4_t r;
   r.x = tl_pack2<BF16>(v[0], v[1]);
@@ -111,10 +121,12 @@ __device__ __forceinline__ u32x4_t tl_dequant8(uint32_t lo, uint32_t hi, float s
 
 // SPLIT: blockIdx.y = z takes slices z ks .. z ks + ks - 1 of K (ks even) and stores its
 // fp32 partial tile to out + z M N (tl_reduce_kernel adds the partials in order).
-template <bool BF16, int OUT_DT, int BM, bool SPLIT>
+// AWQ: the weights are multiplied by awq[k] after the dequant, as the reference does.
+template <bool BF16, bool AWQ, int OUT_DT, int BM, bool SPLIT>
 __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t* __restrict__ x,
                                                                  const uint8_t* __restrict__ nib,
-                                                                 const float* __restrict__ sc, void* __restrict__ out,
+                                                                 const float* __restrict__ sc,
+                                                                 const float* __restrict__ awq, void* __restrict__ out,
                                                                  int M, int N, int K, int n_tiles, int ks) {
   static_assert(!SPLIT || OUT_DT == NVE_DT_F32, "split partials are fp32");
   extern __shared__ __align__(16) char tl_lds[];
@@ -122,7 +134,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   constexpr int WM = BM / 128;    // waves along M (each 128 rows)
   constexpr int TJ = WM;          // 32-column MFMA tiles per wave: BN / (4 / WM) / 32
   constexpr int NX = BM / 32;     // activation transfers (1 KiB) per wave and slice
-  constexpr int TL_X = tl_x_bytes(BM), TL_R0 = tl_r0(BM);
+  constexpr int TL_X = tl_x_bytes(BM), TL_R0 = tl_r0(BM), TL_R = tl_r_bytes(AWQ);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / (4 / WM), wn = wave % (4 / WM);
 
@@ -142,6 +154,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc((void*)nib, (short)0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)sc, (short)0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ar =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(AWQ ? awq : sc), (short)0, 0x7fffffff, 0x00020000);
   // activation transfers: instruction i of wave w fills tile rows (BM / 4) w + 8 i .. + 7
   // (1 KiB); lane l writes row (BM / 4) w + 8 i + l / 8 at chunk position l % 8, i.e. global
   // chunk (l % 8) ^ ((row >> 1) & 7)
@@ -184,6 +198,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     char* const rb = tl_lds + TL_R0 + (2 * rslot + (t & 1)) * TL_R;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(nr, (lds_void_t*)(rb + wave * 1024), 16, noff, tc * 32, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void_t*)(rb + 4096 + wave * 256), 4, soff, tc * 8, 0, 0);
+    // the slice's 64 AWQ factors, one per lane of wave 0 (the others' transfer counts are
+    // unchanged; wave 0 waits for two more per iteration)
+    if (AWQ && wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(rb + 5120), 4, 4u * lane, tc * 256, 0, 0);
   };
   // activation transfers i0 .. i1 - 1 of slice t
   auto issue_x_part = [&](int t, int xslot, int i0, int i1) {
@@ -202,11 +220,13 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     fa[3] = tl_ds_read128<12288>(a);
   };
   // B operand of step kk for one column tile from its raw run q (block kk / 2)
-  auto b_operand = [&](const tl_u2_t& q, float s, int kk) {
+  auto b_operand = [&](const tl_u2_t& q, float s, int kk, const u32x4_t& a0, const u32x4_t& a1) {
     const uint32_t lo = (kk & 1) ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
     const uint32_t hi = (kk & 1) ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-    return tl_dequant8<BF16>(lo, hi, s, -8.0f * s);
+    return tl_dequant8<BF16, AWQ>(lo, hi, s, -8.0f * s, a0, a1);
   };
+  // AWQ factors of the lane's 8 values of step kk: slice values 16 kk + 8 (l / 32) .. + 7
+  const uint32_t aoff = 5120 + 32 * fhi;  // + 64 kk
   // the MFMAs of one slice (activations at LDS xa, raw weights at rb): A fragments of step
   // kk + 1 are read and B operands of step kk + 1 formed while step kk multiplies (each
   // MFMA followed by VALU work); iss(kk) issues transfers of later slices beside the
@@ -216,6 +236,17 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
     tl_u2_t q[2][2];  // [j][block]
     uint32_t sbits[2][2];
     u32x4_t fa[4];
+    u32x4_t aw[4][2] = {};  // AWQ factors of steps 0..3 (unused without AWQ)
+    if constexpr (AWQ) {
+      aw[0][0] = tl_ds_read128<0>(rb + aoff);
+      aw[0][1] = tl_ds_read128<16>(rb + aoff);
+      aw[1][0] = tl_ds_read128<64>(rb + aoff);
+      aw[1][1] = tl_ds_read128<80>(rb + aoff);
+      aw[2][0] = tl_ds_read128<128>(rb + aoff);
+      aw[2][1] = tl_ds_read128<144>(rb + aoff);
+      aw[3][0] = tl_ds_read128<192>(rb + aoff);
+      aw[3][1] = tl_ds_read128<208>(rb + aoff);
+    }
     q[0][0] = tl_ds_read64<0>(rb + bq);
     q[0][1] = tl_ds_read64<16>(rb + bq);
     sbits[0][0] = tl_ds_read32<0>(rb + bs);
@@ -235,6 +266,13 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
         tie(q[j][h]);
         tie(sbits[j][h]);
       }
+    if constexpr (AWQ) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        tie(aw[kk][0]);
+        tie(aw[kk][1]);
+      }
+    }
     float s[2][2];
 #pragma unroll
     for (int j = 0; j < TJ; ++j)
@@ -242,7 +280,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
       for (int h = 0; h < 2; ++h) s[j][h] = __builtin_bit_cast(float, sbits[j][h]);
     u32x4_t fb[2];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) fb[j] = b_operand(q[j][0], s[j][0], 0);
+    for (int j = 0; j < TJ; ++j) fb[j] = b_operand(q[j][0], s[j][0], 0, aw[0][0], aw[0][1]);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk > 0) lgkm_wait();
@@ -259,7 +297,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
       // formed between them
       if (kk < 3) {
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) fb[j] = b_operand(q[j][(kk + 1) >> 1], s[j][(kk + 1) >> 1], kk + 1);
+        for (int j = 0; j < TJ; ++j)
+          fb[j] = b_operand(q[j][(kk + 1) >> 1], s[j][(kk + 1) >> 1], kk + 1, aw[kk + 1][0], aw[kk + 1][1]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -294,7 +333,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4a16_tile_kernel(const uint16_t*
   int xs = 0, rs = 0;  // slots of iteration u's activations and raw weights
   for (int t = 0; t < T; t += 2) {
     const int rs2 = rs == 0 ? 2 : rs - 1;  // (u + 2) % 3 = (u - 1) % 3
-    wait_vmcnt<4>();
+    if (AWQ && wave == 0)
+      wait_vmcnt<6>();
+    else
+      wait_vmcnt<4>();
     lgkm_wait();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -348,9 +390,9 @@ __global__ __launch_bounds__(256) void tl_reduce_kernel(const float* __restrict_
 
 namespace nve_host {
 
-// The tile kernel serves K % 128 == 0 (two slices per iteration) without AWQ, where every
-// byte offset fits its buffer resource (2^31 - 1 bytes; reads past it would return zeros):
-// activations M K, nibbles N K / 2 and scales N K / 8 bytes.
+// The tile kernel serves K % 128 == 0 (two slices per iteration), where every byte offset
+// fits its buffer resource (2^31 - 1 bytes; reads past it would return zeros): activations
+// M K, nibbles N K / 2 and scales N K / 8 bytes (AWQ factors: 4 K).
 long gemm_tile_grid128(int M, int N) {
   return (long)((M + 127) / 128) * ((N + nve::TL_BN - 1) / nve::TL_BN);
 }
@@ -374,15 +416,15 @@ size_t gemm_tile_parts_bytes(int M, int N, int K) {
   return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
 }
 
-bool gemm_tile_fits(int M, int N, int K, bool awq) {
-  return !awq && K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30) && (long)N * (K / 2) < (1L << 31);
+bool gemm_tile_fits(int M, int N, int K, bool /*awq*/) {
+  return K % 128 == 0 && M >= 1 && N >= 1 && (long)M * K < (1L << 30) && (long)N * (K / 2) < (1L << 31);
 }
 
-template <bool BF16, int OUT_DT, int BM, bool SPLIT = false>
-static hipError_t launch_tile_bm(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
-                                 hipStream_t s, int split = 1, int ks = 0) {
-  auto kern = nve::gemm_w4a16_tile_kernel<BF16, OUT_DT, BM, SPLIT>;
-  constexpr int lds = nve::tl_lds_bytes(BM);
+template <bool BF16, bool AWQ, int OUT_DT, int BM, bool SPLIT = false>
+static hipError_t launch_tile_bm(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                                 void* out, int N, int K, hipStream_t s, int split = 1, int ks = 0) {
+  auto kern = nve::gemm_w4a16_tile_kernel<BF16, AWQ, OUT_DT, BM, SPLIT>;
+  constexpr int lds = nve::tl_lds_bytes(BM, AWQ);
   static thread_local int attr_dev = -1;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -393,26 +435,29 @@ static hipError_t launch_tile_bm(const void* x, int M, const uint8_t* nib, const
     attr_dev = dev;
   }
   const int nt = (N + nve::TL_BN - 1) / nve::TL_BN, mt = (M + BM - 1) / BM;
-  hipLaunchKernelGGL(kern, dim3(nt * mt, split), dim3(256), lds, s, (const uint16_t*)x, nib, sc, out, M, N, K, nt, ks);
+  hipLaunchKernelGGL(kern, dim3(nt * mt, split), dim3(256), lds, s, (const uint16_t*)x, nib, sc, awq, out, M, N, K,
+                     nt, ks);
   return hipGetLastError();
 }
 
 // 128-row tiles while their grid is one round (at most one workgroup per CU), else 256
 // (8B gate, fp16 out, us: M = 256 51.4 against 71.2 with 256-row tiles; M = 512 103.3
 // against 81.4, the 128-row grid there being 448 workgroups)
-template <bool BF16, int OUT_DT>
-static hipError_t launch_tile_t(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int N, int K,
-                                hipStream_t s) {
-  if (gemm_tile_grid128(M, N) <= 256) return launch_tile_bm<BF16, OUT_DT, 128>(x, M, nib, sc, out, N, K, s);
-  return launch_tile_bm<BF16, OUT_DT, 256>(x, M, nib, sc, out, N, K, s);
+template <bool BF16, bool AWQ, int OUT_DT>
+static hipError_t launch_tile_t(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                                void* out, int N, int K, hipStream_t s) {
+  if (gemm_tile_grid128(M, N) <= 256)
+    return launch_tile_bm<BF16, AWQ, OUT_DT, 128>(x, M, nib, sc, awq, out, N, K, s);
+  return launch_tile_bm<BF16, AWQ, OUT_DT, 256>(x, M, nib, sc, awq, out, N, K, s);
 }
 
 // With parts (parts_bytes >= gemm_tile_parts_bytes) a small grid is split over K: fp32
 // partials there, added in a fixed order and rounded to out_dt by a second launch.
-template <bool BF16>
-static hipError_t launch_tile_split(const void* x, int M, const uint8_t* nib, const float* sc, void* out, int out_dt,
-                                   int N, int K, float* parts, int split, int ks, hipStream_t s) {
-  hipError_t e = launch_tile_bm<BF16, NVE_DT_F32, 128, true>(x, M, nib, sc, parts, N, K, s, split, ks);
+template <bool BF16, bool AWQ>
+static hipError_t launch_tile_split(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                                   void* out, int out_dt, int N, int K, float* parts, int split, int ks,
+                                   hipStream_t s) {
+  hipError_t e = launch_tile_bm<BF16, AWQ, NVE_DT_F32, 128, true>(x, M, nib, sc, awq, parts, N, K, s, split, ks);
   if (e != hipSuccess) return e;
   const size_t n = (size_t)M * N;
   const dim3 g((unsigned)((n + 255) / 256));
@@ -424,26 +469,33 @@ static hipError_t launch_tile_split(const void* x, int M, const uint8_t* nib, co
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, void* out,
-                                  int out_dt, int N, int K, float* parts, size_t parts_bytes, hipStream_t s) {
-  if (K % (2 * nve::TL_BK) != 0) return hipErrorInvalidValue;
-  const bool bf = x_dt == NVE_DT_BF16;
+template <bool BF16, bool AWQ>
+static hipError_t launch_tile_x(const void* x, int M, const uint8_t* nib, const float* sc, const float* awq,
+                                void* out, int out_dt, int N, int K, float* parts, size_t parts_bytes,
+                                hipStream_t s) {
   if (parts) {
     int ks = 0;
     const int split = tile_split(M, N, K, &ks);
     if (split > 1 && parts_bytes >= (size_t)split * M * N * sizeof(float))
-      return bf ? launch_tile_split<true>(x, M, nib, sc, out, out_dt, N, K, parts, split, ks, s)
-                : launch_tile_split<false>(x, M, nib, sc, out, out_dt, N, K, parts, split, ks, s);
+      return launch_tile_split<BF16, AWQ>(x, M, nib, sc, awq, out, out_dt, N, K, parts, split, ks, s);
   }
-#define NVE_TL(B)                                                                       \
-  switch (out_dt) {                                                                     \
-    case NVE_DT_F16: return launch_tile_t<B, NVE_DT_F16>(x, M, nib, sc, out, N, K, s);   \
-    case NVE_DT_BF16: return launch_tile_t<B, NVE_DT_BF16>(x, M, nib, sc, out, N, K, s); \
-    default: return launch_tile_t<B, NVE_DT_F32>(x, M, nib, sc, out, N, K, s);           \
+  switch (out_dt) {
+    case NVE_DT_F16: return launch_tile_t<BF16, AWQ, NVE_DT_F16>(x, M, nib, sc, awq, out, N, K, s);
+    case NVE_DT_BF16: return launch_tile_t<BF16, AWQ, NVE_DT_BF16>(x, M, nib, sc, awq, out, N, K, s);
+    default: return launch_tile_t<BF16, AWQ, NVE_DT_F32>(x, M, nib, sc, awq, out, N, K, s);
   }
-  if (bf) { NVE_TL(true) }
-  NVE_TL(false)
-#undef NVE_TL
+}
+
+hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
+                                  const float* awq, void* out, int out_dt, int N, int K, float* parts,
+                                  size_t parts_bytes, hipStream_t s) {
+  if (K % (2 * nve::TL_BK) != 0) return hipErrorInvalidValue;
+  const bool bf = x_dt == NVE_DT_BF16;
+  if (awq)
+    return bf ? launch_tile_x<true, true>(x, M, nib, sc, awq, out, out_dt, N, K, parts, parts_bytes, s)
+              : launch_tile_x<false, true>(x, M, nib, sc, awq, out, out_dt, N, K, parts, parts_bytes, s);
+  return bf ? launch_tile_x<true, false>(x, M, nib, sc, awq, out, out_dt, N, K, parts, parts_bytes, s)
+            : launch_tile_x<false, false>(x, M, nib, sc, awq, out, out_dt, N, K, parts, parts_bytes, s);
 }
 
 }  // namespace nve_host

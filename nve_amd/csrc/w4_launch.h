@@ -219,14 +219,15 @@ hipError_t launch_w4a8_fused(int src, int pair, const nve::ProdArgs& pa, const W
                              hipStream_t stream, const nve::EpiArgs& ra);
 hipError_t launch_w4a16_fused(int src, int pair, const nve::ProdArgs& pa, const W4Segs& segs, int out_dt, int K,
                               hipStream_t stream, const nve::EpiArgs& ra);
-// Large-M W4A16 GEMM (gemm_w4a16_tile.hip): K % 128 == 0, no AWQ, M K < 2^30,
-// N K / 2 < 2^31; gemm_tile_grid128 = its workgroup count with 128-row tiles.
+// Large-M W4A16 GEMM (gemm_w4a16_tile.hip): K % 128 == 0, M K < 2^30, N K / 2 < 2^31;
+// gemm_tile_grid128 = its workgroup count with 128-row tiles.
 bool gemm_tile_fits(int M, int N, int K, bool awq);
 long gemm_tile_grid128(int M, int N);
 // fp32 partial bytes of its K split where the 128-row grid leaves CUs idle (0: no split)
 size_t gemm_tile_parts_bytes(int M, int N, int K);
-hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc, void* out,
-                                  int out_dt, int N, int K, float* parts, size_t parts_bytes, hipStream_t s);
+hipError_t launch_gemm_w4a16_tile(const void* x, int x_dt, int M, const uint8_t* nib, const float* sc,
+                                  const float* awq, void* out, int out_dt, int N, int K, float* parts,
+                                  size_t parts_bytes, hipStream_t s);
 hipError_t launch_embed(const uint16_t* embed, const int* token, float* hidden, int H, int vocab, hipStream_t s);
 hipError_t launch_w4a8(const int8_t* xq, const float* xs, const W4Segs& segs, int out_dt, int K,
                        hipStream_t stream);

@@ -119,9 +119,10 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
 @pytest.mark.parametrize("m,n,k", [(330, 130, 256), (321, 1000, 512), (130, 16000, 256), (1100, 300, 1024),
                                    (600, 8200, 256), (513, 4100, 512), (300, 200, 192)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
-def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n, k, xdt):
-    """Without AWQ and with K % 128 == 0 the tile kernel (gemm_w4a16_tile.hip) runs above
-    320 rows, and from 128 rows where its 128-row grid has at least 128 workgroups; it
+@pytest.mark.parametrize("with_awq", [False, True])
+def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n, k, xdt, with_awq):
+    """With K % 128 == 0 the tile kernel (gemm_w4a16_tile.hip) runs above 320 rows (with
+    AWQ above 128), and from 128 rows where its 128-row grid has at least 128 workgroups; it
     takes 128-row tiles while that grid has at most 256 workgroups, else 256-row tiles
     (here: 128 rows at 3 x 2, 3 x 8, 2 x 125, 9 x 3 and 5 x 33 tiles, 256 rows at 3 x 65;
     K % 128 == 64, here K = 192, runs the 128 x 128-tile kernel).  One-hot activation rows
@@ -129,25 +130,28 @@ def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n,
     column k_i as the kernel rounded it, which must equal the reference dequant bit for
     bit.  Ragged M and N, K = 256 (one iteration of two slices), and tile grids that are
     not a multiple of 8 workgroups (the XCD-grouped tile order); fp32 output, and fp16 /
-    bf16 output for fp16 / bf16 x (exact too)."""
+    bf16 output for fp16 / bf16 x (exact too).  With AWQ every weight is the reference's
+    f32 dequant times awq[k], then rounded."""
     torch = torch_dev
-    print(f"tile identity m={m} n={n} k={k} x={xdt}", flush=True)
+    print(f"tile identity m={m} n={n} k={k} x={xdt} awq={with_awq}", flush=True)
     data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.3))
     nib, sc = orc.extract_for_gpu(data, n, k)
-    wref = _round(orc.q4_to_f32(data, n, k, None), xdt)
+    awq = np.random.default_rng(n + k).uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
+    wref = _round(orc.q4_to_f32(data, n, k, awq), xdt)
+    ta = None if awq is None else torch.from_numpy(awq).cuda()
     ks = np.random.default_rng(m + k).integers(0, k, m)
     tdt = torch.float16 if xdt == "f16" else torch.bfloat16
     x = torch.zeros((m, k), dtype=tdt, device="cuda")
     x[torch.arange(m, device="cuda"), torch.from_numpy(ks).cuda()] = 1
     tn, ts = torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda()
-    y = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.float32)
+    y = hk.gemm_w4a16(x, tn, ts, n, k, ta, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy().view(np.uint32), np.ascontiguousarray(wref[:, ks].T).view(np.uint32))
     if xdt == "f16":
-        y16 = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.float16)
+        y16 = hk.gemm_w4a16(x, tn, ts, n, k, ta, out_dtype=torch.float16)
         assert np.array_equal(y16.cpu().numpy(), wref[:, ks].T.astype(np.float16))
     else:
-        yb = hk.gemm_w4a16(x, tn, ts, n, k, out_dtype=torch.bfloat16)
+        yb = hk.gemm_w4a16(x, tn, ts, n, k, ta, out_dtype=torch.bfloat16)
         assert np.array_equal(yb.float().cpu().numpy().view(np.uint32),
                               np.ascontiguousarray(wref[:, ks].T).view(np.uint32))
 
@@ -300,7 +304,8 @@ def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
 @pytest.mark.parametrize("m,n,k", [(200, 520, 2048), (300, 1000, 1152), (130, 4100, 8192), (513, 300, 1024),
                                    (100, 520, 2048), (65, 4101, 1024)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
-def test_gemm_w4a16_ws_tile_split(orc, torch_dev, hk, m, n, k, xdt):
+@pytest.mark.parametrize("with_awq", [False, True])
+def test_gemm_w4a16_ws_tile_split(orc, torch_dev, hk, m, n, k, xdt, with_awq):
     """With a workspace, the register-dequant tile kernel splits K where its 128-row grid
     leaves CUs idle, from M = 65 (here 2 x 5 tiles in 4 splits, 3 x 8 in 2 of 10 and 8
     slices, 2 x 33 in 3 of 44, 44 and 40, 5 x 3 in 2, 1 x 5 in 4, 1 x 33 in 2 with an odd
@@ -308,39 +313,42 @@ def test_gemm_w4a16_ws_tile_split(orc, torch_dev, hk, m, n, k, xdt):
     x's): each split stores fp32 partials, one more launch adds them in split order and
     rounds once to the output type.  Every call and every graph replay gives the same
     bits; an fp16 / bf16 output is exactly the fp32 result rounded; the product is within
-    fp32 rounding of the unsplit one and within the W4A16 bar of the oracle."""
+    fp32 rounding of the unsplit one and within the W4A16 bar of the oracle; with and
+    without AWQ."""
     torch = torch_dev
-    print(f"tile split m={m} n={n} k={k} x={xdt}", flush=True)
+    print(f"tile split m={m} n={n} k={k} x={xdt} awq={with_awq}", flush=True)
     wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
     assert wsb >= 2 * m * n * 4
     data = orc.q4_from_f32(weights(n, k, seed=m + n, std=0.05))
     nib_h, sc_h = orc.extract_for_gpu(data, n, k)
     nib, sc = torch.from_numpy(nib_h).cuda(), torch.from_numpy(sc_h).cuda()
+    awq = np.random.default_rng(n).uniform(0.5, 2.0, k).astype(np.float32) if with_awq else None
+    ta = None if awq is None else torch.from_numpy(awq).cuda()
     xr = _round(np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32), xdt)
     tdt = torch.float16 if xdt == "f16" else torch.bfloat16
     x = torch.from_numpy(xr).cuda().to(tdt)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     if m <= 512:
-        a = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws)
-        assert torch.equal(a, hk.gemm_w4a16_ws(x, nib, sc, n, k, ws))
-        unsplit = hk.gemm_w4a16(x, nib, sc, n, k)
+        a = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, ta)
+        assert torch.equal(a, hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, ta))
+        unsplit = hk.gemm_w4a16(x, nib, sc, n, k, ta)
         assert torch.allclose(a, unsplit, rtol=1e-5, atol=1e-5 * float(a.abs().max()))
-        wref = _round(orc.q4_to_f32(data, n, k, None), xdt).astype(np.float64)
+        wref = _round(orc.q4_to_f32(data, n, k, awq), xdt).astype(np.float64)
         assert rel_err_floor(a.cpu().numpy(), xr.astype(np.float64) @ wref.T) <= 2e-3
         for odt in (torch.float16, torch.bfloat16):
-            assert torch.equal(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=odt), a.to(odt))
+            assert torch.equal(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, ta, out_dtype=odt), a.to(odt))
     else:
         odt = torch.bfloat16 if xdt == "f16" else torch.float16  # not BLAS-eligible: fused
-        a = hk.gemm_w4a16(x, nib, sc, n, k).to(odt)
-        b = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=odt)
+        a = hk.gemm_w4a16(x, nib, sc, n, k, ta).to(odt)
+        b = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, ta, out_dtype=odt)
         assert torch.allclose(a.float(), b.float(), rtol=2 ** -7, atol=1e-5 * float(a.float().abs().max()))
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
-    ref16 = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16)
+    ref16 = hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, ta, out_dtype=torch.float16)
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        out.copy_(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, out_dtype=torch.float16))
+        out.copy_(hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, ta, out_dtype=torch.float16))
     for _ in range(3):
         out.zero_()
         g.replay()
