@@ -227,10 +227,10 @@ int nve_hip_dequant_w4(const uint8_t *nibbles, const float *scales, const float 
  * then a dense GEMM) in one kernel: each weight is rounded exactly as the dequant
  * rounds it (to x's dtype: F16 as the reference, or BF16) and the products accumulate
  * in fp32 on MFMA (M <= 320: weight-streaming kernels, where K % 128 == 0 and N <= 16384 an
- * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; without awq and
- * with K % 128 == 0, 128 x 128 or 256 x 128 output tiles with the weights dequantized in
- * registers above M = 320, and from M = 128 where N / 128 * M / 128 >= 128 tiles;
- * otherwise 128 x 128 tiles dequantized in LDS).  x [M, K]
+ * LDS ring in launches of up to 64 rows (32 with awq), else M <= 16 only; with K % 128 ==
+ * 0, 128 x 128 or 256 x 128 output tiles with the weights dequantized in registers above
+ * M = 320 (128 with awq), and from M = 128 (65 with awq) where N / 128 * M / 128 >= 96
+ * tiles; otherwise 128 x 128 tiles dequantized in LDS).  x [M, K]
  * row-major F16/BF16 (16-byte aligned); awq [K] or NULL; out [M, N] row-major F16,
  * BF16 or F32.  K % 64 == 0.  Bit-reproducible: the same inputs give the same bits on
  * every call (no atomic accumulation; nve_hip_gemm_w4a16_ws can also split K over

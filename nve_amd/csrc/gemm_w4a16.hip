@@ -774,7 +774,7 @@ hipError_t launch_gemm_w4a16_parts(const void* x, int x_dt, int M, const uint8_t
                                    const float* awq, void* out, int out_dt, int N, int K, float* parts,
                                    size_t parts_bytes, hipStream_t s) {
   const bool bf = x_dt == NVE_DT_BF16;
-  // from M = 128 (no AWQ, K % 128 == 0) the 128- / 256-row tile kernel of
+  // from M = 128 (K % 128 == 0) the 128- / 256-row tile kernel of
   // gemm_w4a16_tile.hip (with AWQ from M = 65); with K-split partials from M = 65.  Without
   // them it runs up to the ring launches' range (320 rows, AWQ 128) only where its 128-row
   // grid has at least 96 workgroups: one workgroup streams all of K, so a narrow grid

@@ -3,7 +3,8 @@
 // accumulation.  Same product as the reference's prefill path (GpuWeight::matmul_x,
 // src/gpu_layer.rs:219-237: nve_dequant_w4a16, cuda/nve_kernels.cu:397-433, then a dense
 // GEMM), with every weight dequantized exactly as that dequant rounds it
-// (f32 fma(n, s, -8 s) = (n - 8) s, then RNE to the activation type) but only in registers.
+// (f32 fma(n, s, -8 s) = (n - 8) s [times awq[k] in f32], then RNE to the activation type)
+// but only in registers.
 //
 // Tile: 256 x 128 outputs per workgroup of 4 waves (2 x 2), 128 x 64 per wave as 4 x 2
 // tiles of v_mfma_f32_32x32x16, or 128 x 128 outputs as 4 waves (1 x 4) of 128 x 32 (4 x 1
