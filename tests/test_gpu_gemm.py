@@ -156,6 +156,24 @@ def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n,
                               np.ascontiguousarray(wref[:, ks].T).view(np.uint32))
 
 
+def test_gemm_w4a16_tile_wide_n_exact(orc, torch_dev, hk):
+    """The tile kernel at an lm_head-wide N (128256 rows of weights, 1002 column tiles):
+    at M = 300 its 256-row grid is 2 x 1002 workgroups, about eight rounds on 256 CUs,
+    with the XCD-grouped order spread over them.  One-hot activation rows: every output
+    is one weight as the reference dequant rounds it, compared bit for bit."""
+    torch = torch_dev
+    m, n, k = 300, 128256, 256
+    data = orc.q4_from_f32(weights(n, k, seed=77, std=0.3))
+    nib, sc = orc.extract_for_gpu(data, n, k)
+    wref = orc.q4_to_f32(data, n, k, None).astype(np.float16)
+    ks = np.random.default_rng(78).integers(0, k, m)
+    x = torch.zeros((m, k), dtype=torch.float16, device="cuda")
+    x[torch.arange(m, device="cuda"), torch.from_numpy(ks).cuda()] = 1
+    y = hk.gemm_w4a16(x, torch.from_numpy(nib).cuda(), torch.from_numpy(sc).cuda(), n, k, out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), np.ascontiguousarray(wref[:, ks].T))
+
+
 @pytest.mark.parametrize("odt,tol", [("bf16", 2.0 ** -8 + 2e-3), ("f16", 2.0 ** -11 + 2e-3)])
 @pytest.mark.parametrize("m", [33, 5, 130, 300])
 def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
