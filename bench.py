@@ -652,7 +652,8 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
     Times: HIP events over graphs of `reps` launches; TFLOP/s = 2 M N K / time.
     library_us: nve_hip_gemm_w4a16_ws with its workspace (dequant + hipBLASLt above
     M = 512, the fused kernels up to it), fp32 output; library_f16_out_us: the same
-    with fp16 output, the output type of the reference-method timing."""
+    with fp16 output, the output type of the reference-method timing.  awq_rows: the
+    library entry and the two-step method with AWQ factors at M = 128 and 512."""
     g = torch.Generator(device="cuda").manual_seed(17)
     n, k = 14336, 4096
     nib, sc = hk.q4_quantize(torch.randn((n, k), generator=g, device="cuda").mul_(0.02))
@@ -695,6 +696,20 @@ def prefill_gemm(torch, hk, reps: int = 20) -> dict:
                             "library_path": "dequant + hipBLASLt" if m > 512 and wsb else "fused"})
         log(f"  prefill GEMM M={m}: {us:.1f} us ({fl / us / 1e6:.0f} TFLOP/s), dequant+BLAS {us_ref:.1f} us, "
             f"nve_hip_gemm_w4a16_ws {us_lib:.1f} us (fp16 out {us_lib16:.1f} us)")
+        del x, wf, ws
+    # with AWQ factors (the reference dequant multiplies each f32 weight by awq[k] before the
+    # fp16 rounding): the library entry with its workspace against the same two-step method
+    awq = torch.rand(k, generator=g, device="cuda").add_(0.5)
+    out["awq_rows"] = []
+    for m in (128, 512):
+        x = torch.randn((m, k), generator=g, device="cuda").half()
+        wf = hk.dequant_w4(nib, sc, n, k, awq)
+        wsb = hk.gemm_w4a16_workspace_bytes(m, n, k)
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda") if wsb else None
+        us_lib = timed(lambda: hk.gemm_w4a16_ws(x, nib, sc, n, k, ws, awq))
+        us_ref = timed(lambda: hk.dequant_w4(nib, sc, n, k, awq)) + timed(lambda: torch.matmul(x, wf.t()))
+        out["awq_rows"].append({"M": m, "library_us": round(us_lib, 1), "dequant_plus_blas_us": round(us_ref, 1)})
+        log(f"  prefill GEMM with AWQ M={m}: nve_hip_gemm_w4a16_ws {us_lib:.1f} us, dequant+BLAS {us_ref:.1f} us")
         del x, wf, ws
     return out
 

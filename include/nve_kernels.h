@@ -242,9 +242,9 @@ int nve_hip_gemm_w4a16(const void *x, int x_dtype, int M, const uint8_t *nibbles
 /* The same product with the reference's own two-step method where it is faster
  * (GpuWeight::matmul_x, src/gpu_layer.rs:219-237), and bit-reproducible everywhere.
  * The workspace (nve_hip_gemm_w4a16_workspace_bytes(M, N, K) bytes, 256-byte aligned)
- * holds: for M > 512, with out F32 or x's dtype, the weights dequantized by
- * nve_hip_dequant_w4 (bit-identical to the reference dequant), which hipBLASLt then
- * multiplies with fp32 accumulation; otherwise the fp32 partials of the fused kernels'
+ * holds: for M > 512 (M > 384 with awq), with out F32 or x's dtype, the weights
+ * dequantized by nve_hip_dequant_w4 (bit-identical to the reference dequant), which
+ * hipBLASLt then multiplies with fp32 accumulation; otherwise the fp32 partials of the fused kernels'
  * K split where their tile grid leaves CUs idle, added in a fixed order and rounded once
  * to out_dtype (0 bytes when the shape does not split).  With a NULL
  * or smaller workspace it runs nve_hip_gemm_w4a16.  The first call per device and

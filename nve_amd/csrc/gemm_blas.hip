@@ -32,9 +32,13 @@ size_t gemm_split_parts_bytes(int M, int N, int K);
 
 namespace {
 
-// from here on dequant + GEMM is faster (8B gate, fp16 out: 102.5 us at M = 640 against
-// 165.6 for the tile kernel; at M = 512 the tile kernel's 83.6 beats its 94.1)
+// from here on dequant + GEMM is faster (fp16 out, us: 8B gate M = 640 96.8 against 145.9
+// for the tile kernel, 8B down 116.2 against 135.5; at M = 384-512 the two are within 10%,
+// the tile kernel ahead at down); with AWQ factors from 385 rows, where the tile kernel's
+// extra multiply and factor reads put it behind at the gate (fp32 out, M = 512: 88.0 against
+// 80.8; down 103.1 against 104.5)
 constexpr int kGemmBlasMinM = 513;
+constexpr int kGemmBlasMinMAwq = 385;
 constexpr size_t kBlasWorkspace = 32u << 20;
 constexpr int kBlasCandidates = 32;  // heuristic candidates timed on the first call per shape
 constexpr int kBlasTimedRuns = 5;    // timed runs per candidate (after one untimed run)
@@ -140,17 +144,19 @@ AlgoChoice select_algo(hipblasLtHandle_t h, const Descs& ds, const void* x, void
 
 }  // namespace
 
-// Below kGemmBlasMinM: the fp32 partials of the fused kernel's K split (0 when that
-// shape does not split); from it on: the dequantized weights + the hipBLASLt workspace.
+// Below kGemmBlasMinMAwq: the fp32 partials of the fused kernels' K split (0 when that
+// shape does not split); from it on also room for the dequantized weights + the hipBLASLt
+// workspace (used from kGemmBlasMinM, or kGemmBlasMinMAwq with AWQ factors).
 size_t gemm_w4a16_ws_bytes(int M, int N, int K) {
-  if (M < kGemmBlasMinM) return round256(gemm_split_parts_bytes(M, N, K));
+  if (M < kGemmBlasMinMAwq) return round256(gemm_split_parts_bytes(M, N, K));
   const size_t blas = round256((size_t)N * K * 2) + kBlasWorkspace;
   const size_t parts = round256(gemm_split_parts_bytes(M, N, K));
   return blas > parts ? blas : parts;
 }
 
-// Dequant + hipBLASLt when M >= kGemmBlasMinM, the workspace is large enough and the
-// output is F32 or x's dtype; otherwise the fused kernel.  The first call per device and
+// Dequant + hipBLASLt when M >= kGemmBlasMinM (kGemmBlasMinMAwq with AWQ factors), the
+// workspace is large enough and the output is F32 or x's dtype; otherwise the fused
+// kernel.  The first call per device and
 // shape creates the hipBLASLt handle and picks the fastest of up to kBlasCandidates
 // heuristic algorithms by timing them on the caller's stream; under graph capture a
 // device or shape without that state takes the fused kernel instead.
@@ -162,7 +168,8 @@ hipError_t launch_gemm_w4a16_ws(const void* x, int x_dt, int M, const uint8_t* n
   auto fused = [&]() {
     return launch_gemm_w4a16_parts(x, x_dt, M, nib, sc, awq, out, out_dt, N, K, (float*)ws, ws ? ws_bytes : 0, s);
   };
-  const size_t need = M >= kGemmBlasMinM ? round256((size_t)N * K * 2) + kBlasWorkspace : 0;
+  const int blas_min = awq ? kGemmBlasMinMAwq : kGemmBlasMinM;
+  const size_t need = M >= blas_min ? round256((size_t)N * K * 2) + kBlasWorkspace : 0;
   if (need == 0 || ws == nullptr || ws_bytes < need || (out_dt != NVE_DT_F32 && out_dt != x_dt)) return fused();
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);

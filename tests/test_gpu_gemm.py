@@ -198,6 +198,16 @@ def test_gemm_w4a16_rounded_outputs(orc, torch_dev, hk, odt, tol, m):
 def test_gemm_w4a16_ws_blas_path(orc, torch_dev, hk, m, n, k, xdt, with_awq):
     """nve_hip_gemm_w4a16_ws above M = 512 with its workspace: dequant (bit-identical
     weights) + hipBLASLt, the reference's own prefill method, to the same bar."""
+    _ws_blas_check(orc, torch_dev, hk, m, n, k, xdt, with_awq)
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_gemm_w4a16_ws_blas_path_awq_from_385(orc, torch_dev, hk, xdt):
+    """With AWQ factors the workspace path takes dequant + hipBLASLt from M = 385."""
+    _ws_blas_check(orc, torch_dev, hk, 400, 256, 1024, xdt, True)
+
+
+def _ws_blas_check(orc, torch_dev, hk, m, n, k, xdt, with_awq):
     torch = torch_dev
     print(f"gemm_ws m={m} n={n} k={k} x={xdt} awq={with_awq}", flush=True)
     rng = np.random.default_rng(m + 3 * n + k)
@@ -226,14 +236,15 @@ def test_gemm_w4a16_ws_blas_path(orc, torch_dev, hk, m, n, k, xdt, with_awq):
 
 
 def test_gemm_w4a16_ws_falls_back(orc, torch_dev, hk):
-    """Up to M = 512, or without a workspace, nve_hip_gemm_w4a16_ws is the fused kernel
+    """Up to M = 512 (no AWQ factors), or without a workspace, nve_hip_gemm_w4a16_ws is the fused kernel
     (compared at fp16 output: with a workspace an fp32 product at small M splits K, whose
     partials then add in a different order than one pass)."""
     torch = torch_dev
-    # up to M = 512 the workspace holds only K-split partials (none for M <= 16)
+    # up to M = 384 the workspace holds only K-split partials (none for M <= 16); from 385
+    # also room for the dequantized weights (used with AWQ factors up to 512, else above)
     assert hk.gemm_w4a16_workspace_bytes(16, 256, 1024) == 0
-    assert hk.gemm_w4a16_workspace_bytes(511, 256, 1024) == 4 * 511 * 256 * 4
-    assert hk.gemm_w4a16_workspace_bytes(512, 256, 1024) == 4 * 512 * 256 * 4
+    assert hk.gemm_w4a16_workspace_bytes(384, 256, 1024) == 4 * 384 * 256 * 4
+    assert hk.gemm_w4a16_workspace_bytes(385, 256, 1024) > (256 * 1024 * 2)
     assert hk.gemm_w4a16_workspace_bytes(513, 256, 1024) > (256 * 1024 * 2)
     n, k = 256, 1024
     data = orc.q4_from_f32(weights(n, k, seed=5, std=0.05))
