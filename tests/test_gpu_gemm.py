@@ -117,7 +117,7 @@ def test_gemm_w4a16_small_m_weights_match_dequant_exactly(orc, torch_dev, hk, xd
 
 
 @pytest.mark.parametrize("m,n,k", [(330, 130, 256), (321, 1000, 512), (130, 16000, 256), (1100, 300, 1024),
-                                   (600, 8200, 256), (513, 4100, 512), (300, 200, 192)])
+                                   (600, 8200, 256), (513, 4100, 512), (300, 200, 192), (330, 200, 128)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n, k, xdt, with_awq):
@@ -128,7 +128,8 @@ def test_gemm_w4a16_tile_weights_match_dequant_exactly(orc, torch_dev, hk, m, n,
     K % 128 == 64, here K = 192, runs the 128 x 128-tile kernel).  One-hot activation rows
     (row i picks column k_i) make each output one product 1 * w, so Y[i, :] is weight
     column k_i as the kernel rounded it, which must equal the reference dequant bit for
-    bit.  Ragged M and N, K = 256 (one iteration of two slices), and tile grids that are
+    bit.  Ragged M and N, K = 256 (two iterations of two 64-wide slices) and K = 128 (one
+    iteration, every later slice's transfers clamped to its last slice), and tile grids that are
     not a multiple of 8 workgroups (the XCD-grouped tile order); fp32 output, and fp16 /
     bf16 output for fp16 / bf16 x (exact too).  With AWQ every weight is the reference's
     f32 dequant times awq[k], then rounded."""
