@@ -332,14 +332,14 @@ def test_gemm_w4a16_ws_split_k_reproducible(orc, torch_dev, hk, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(200, 520, 2048), (300, 1000, 1152), (130, 4100, 8192), (513, 300, 1024),
-                                   (100, 520, 2048), (65, 4101, 1024)])
+                                   (100, 520, 2048), (65, 4101, 1024), (130, 520, 2688)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16"])
 @pytest.mark.parametrize("with_awq", [False, True])
 def test_gemm_w4a16_ws_tile_split(orc, torch_dev, hk, m, n, k, xdt, with_awq):
     """With a workspace, the register-dequant tile kernel splits K where its 128-row grid
     leaves CUs idle, from M = 65 (here 2 x 5 tiles in 4 splits, 3 x 8 in 2 of 10 and 8
     slices, 2 x 33 in 3 of 44, 44 and 40, 5 x 3 in 2, 1 x 5 in 4, 1 x 33 in 2 with an odd
-    M N; M = 513 takes the fused path when the output type is neither fp32 nor
+    M N, 2 x 5 in 5 of 10, 10, 10, 10 and 2 slices; M = 513 takes the fused path when the output type is neither fp32 nor
     x's): each split stores fp32 partials, one more launch adds them in split order and
     rounds once to the output type.  Every call and every graph replay gives the same
     bits; an fp16 / bf16 output is exactly the fp32 result rounded; the product is within
