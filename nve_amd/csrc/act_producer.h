@@ -215,14 +215,6 @@ __device__ __forceinline__ uint4 prod_f16x8(const float (&v)[8]) {
   return make_uint4(d[0], d[1], d[2], d[3]);
 }
 
-__device__ __forceinline__ uint4 prod_bf16x8(const float (&v)[8]) {
-  uint32_t d[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-    d[t] = (uint32_t)f32_to_bf16_bits(v[2 * t]) | ((uint32_t)f32_to_bf16_bits(v[2 * t + 1]) << 16);
-  return make_uint4(d[0], d[1], d[2], d[3]);
-}
-
 }  // namespace nve
 
 namespace nve {

@@ -34,7 +34,13 @@ constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64, GM_LD = GM_BK + 8;
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if (BF16) return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+  if (BF16) {
+    // one v_cvt_pk_bf16_f32 (round to nearest even) of the materialised f32 values
+    typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+    asm volatile("" : "+v"(a), "+v"(b));
+    const bf2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
   return (uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(a)) |
          ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(b)) << 16);
 }

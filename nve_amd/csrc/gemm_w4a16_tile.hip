@@ -53,6 +53,7 @@ typedef __bf16 tl_b8_t __attribute__((ext_vector_type(8)));
 typedef float tl_f16x_t __attribute__((ext_vector_type(16)));
 typedef float tl_f2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 tl_h2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 tl_b2_t __attribute__((ext_vector_type(2)));
 typedef unsigned int tl_u2_t __attribute__((ext_vector_type(2)));
 
 template <bool BF16>
@@ -85,10 +86,10 @@ __device__ __forceinline__ uint32_t tl_ds_read32(uint32_t a) {
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t tl_pack2(float a, float b) {
-  if (BF16) return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
-  // each value is an f32 first (the fma's rounding), then one v_cvt_pk_f16_f32 (round to
-  // nearest even): the reference dequant's two roundings
+  // each value is an f32 first (the fma's rounding), then one v_cvt_pk_{f16,bf16}_f32
+  // (round to nearest even): the reference dequant's two roundings
   asm("" : "+v"(a), "+v"(b));
+  if (BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector((tl_f2_t){a, b}, tl_b2_t));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((tl_f2_t){a, b}, tl_h2_t));
 }
 // The reference dequant of 8 nibbles -- one per byte of lo (values 0..3) and hi (values

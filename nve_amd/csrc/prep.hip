@@ -329,9 +329,11 @@ __global__ __launch_bounds__(256) void dequant_w4_kernel(const uint8_t* __restri
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const float a = v[2 * t], b = v[2 * t + 1];
-      if (OUT_DT == NVE_DT_BF16)
-        p[t] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
-      else
+      if (OUT_DT == NVE_DT_BF16) {
+        typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+        const bf2_t h = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32, round to nearest even
+        p[t] = __builtin_bit_cast(uint32_t, h);
+      } else
         p[t] = (uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(a)) |
                ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_rne(b)) << 16);
     }
